@@ -1,0 +1,195 @@
+"""Benchmark of the quantized TBE inference forward on one MI355X.
+
+Workload (the INT4 26-table DLRM shape the metric is quoted on):
+26 tables x 4M rows, D=128, INT4 rowwise (80-byte padded rows), B=8192,
+bag length Poisson(30) clipped to [1,100], Zipf(1.05) indices (ranks scattered by a
+random permutation per table), int32 indices/offsets, SUM pooling, fp16 output
+[8192, 3328].  A "step" is one call of
+torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function over that batch,
+with every input resident in HBM before the timed region starts.
+
+Prints ONE JSON line.  `value` = pooled lookups per second; `roofline` prices the
+kernel's algorithmic bytes (unpadded rows of every lookup + indices + offsets +
+output) per launch against the 8 TB/s HBM peak; `cpu_baseline` times the C oracle
+(OpenMP) on a bounded sample of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, help="benchmark configuration id (0-4)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target wall time of the CPU leg")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache measurement")
+    ap.add_argument("--flags", type=int, default=0, help="TBE_FLAG_* tuning switches (C-ABI path)")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "tbe_int4_cfg2_traffic.json"),
+                    help="HBM traffic per launch measured with rocprofv3 --pmc (JSON)")
+    return ap.parse_args()
+
+
+def _cpu_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(wl, target_s: float):
+    """Time the C oracle on a bounded sample of the workload (whole bags, all tables)."""
+    import numpy as np
+    import torch
+    import __graft_entry__ as graft
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _parity import compact_problem, run_oracle
+
+    oracle = graft.load_oracle()
+    cores = min(_cpu_cores(), 16)
+    B = wl.spec.B
+    nsamp = max(1, B // 8)
+    g = torch.Generator(device=wl.indices.device)
+    g.manual_seed(17)
+    b_sel = torch.randperm(B, device=wl.indices.device, generator=g)[:nsamp].sort().values
+    prob = compact_problem(wl.module, wl.indices, wl.offsets, wl.per_sample_weights, b_sel)
+    n_lookups = int(prob["offsets"][-1])
+    pm = int(wl.module.pooling_mode)
+    run_oracle(oracle, prob, pm, wl.module.output_dtype)  # warm the host caches / page in
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        bits, bias = prob["fp8"]
+        oracle.forward(prob["weights"], prob["weights_offsets"], prob["weights_tys"], prob["D_offsets"],
+                       prob["indices"], prob["offsets"], pm, prob["psw"], wl.module.output_dtype,
+                       fp8_exponent_bits=bits, fp8_exponent_bias=bias, num_threads=cores)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s or reps >= 1000:
+            break
+    rate = n_lookups * reps / el
+    return {"value": rate, "unit": "pooled lookups/s", "cores": cores, "kind": "port",
+            "sample": f"{nsamp} of {B} samples x {len(wl.module.specs)} tables "
+                      f"({n_lookups} lookups, rows gathered to host), {reps} reps in {el:.1f}s, "
+                      f"oracle/tbe_oracle.c OpenMP fp32"}
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards table-wise across GPUs by design but no multi-GPU run is provided.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as graft
+    pkg = graft.load_package()
+    from fbgemm_ascend_amd.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = make_workload(args.config, device=dev)
+    m = wl.module
+    torch.cuda.synchronize()
+
+    if args.flags:
+        def step():
+            return pkg.capi.forward_tensors(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets,
+                                            wl.indices, wl.offsets, int(m.pooling_mode),
+                                            wl.per_sample_weights, m.output_dtype, flags=args.flags)
+    else:
+        step = wl.run
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_call_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    kernel_ms = sum(per_call_ms) / len(per_call_ms)
+    ms_per_step = wall * 1e3 / args.steps
+
+    cold_ms = None
+    if not args.no_cold:
+        scrub = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
+        cold = []
+        for i in range(min(args.steps, 20)):
+            scrub.fill_(i & 0xFF)  # evict L2 and MALL between calls
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            step()
+            b.record(stream)
+            torch.cuda.synchronize()
+            cold.append(a.elapsed_time(b))
+        cold_ms = sorted(cold)[len(cold) // 2]
+        del scrub
+
+    N = wl.num_indices
+    bags = wl.num_bags
+    alg_bytes = wl.algorithmic_bytes()
+    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            t = json.load(f)
+        if t.get("config") == args.config:
+            traffic = t.get("hbm_bytes_per_launch")
+
+    res = {
+        "metric": "pooled lookups/sec + achieved HBM GB/s (% roofline), INT4/INT8 TBE fwd, 1 GPU",
+        "value": N / (ms_per_step * 1e-3),
+        "unit": "pooled lookups/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {2: "int8", 3: "int4"}.get(int(m.specs[0][2]), "mixed") if args.config != 3 else "mixed",
+        "data": "synthetic (seeded, generated on device)",
+        "config": {"workload": f"config{args.config}: {wl.spec.description}",
+                   "tables": len(m.specs), "rows_per_table": m.specs[0][0] if args.config != 3 else "mixed",
+                   "D": m.specs[0][1] if args.config != 3 else "mixed", "batch": wl.spec.B,
+                   "bag_len": wl.spec.bag_len, "zipf_alpha": wl.spec.zipf_alpha,
+                   "index_dtype": str(wl.indices.dtype).replace("torch.", ""),
+                   "pooling": wl.spec.pooling.name, "output": {0: "fp32", 1: "fp16", 5: "bf16"}[m.output_dtype],
+                   "lookups_per_step": N, "bags_per_step": bags},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
+        "kernel_ms": kernel_ms,
+        "kernel_ms_median": per_call_ms[len(per_call_ms) // 2],
+        "cold_cache_kernel_ms": cold_ms,
+        "algorithmic_bytes_per_step": alg_bytes,
+        "bags_per_s": bags / (ms_per_step * 1e-3),
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,81 @@
+"""fbgemm-ascend_amd: MI355X-native quantized TBE inference forward.
+
+Importing the package makes torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function
+run on HIP tensors, like `import fbgemm_ascend` does for NPU tensors (reference
+fbgemm_ascend/__init__.py:9 and :189-231).  The reference relies on fbgemm_gpu
+to define the op schema; when fbgemm_gpu is absent this package defines the
+identical schema itself.
+
+The directory name contains a hyphen, so load it with `load_package()` below
+(or importlib) under the module name `fbgemm_ascend_amd`.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+__version__ = "0.1.0"
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+HIP_LIB = os.path.join(PKG_DIR, "libtbe_hip.so")
+TORCH_LIB = os.path.join(PKG_DIR, "_tbe_torch.so")
+
+OP_NAME = "int_nbit_split_embedding_codegen_lookup_function"
+# Same schema as fbgemm_gpu's (reference call site T:94-118, adapter A:55-78).
+OP_SCHEMA = (
+    "int_nbit_split_embedding_codegen_lookup_function("
+    "Tensor dev_weights, Tensor uvm_weights, Tensor weights_placements, Tensor weights_offsets, "
+    "Tensor weights_tys, Tensor D_offsets, int total_D, int max_int2_D, int max_int4_D, "
+    "int max_int8_D, int max_float16_D, int max_float32_D, Tensor indices, Tensor offsets, "
+    "int pooling_mode, Tensor? indice_weights, int output_dtype, Tensor? lxu_cache_weights, "
+    "Tensor? lxu_cache_locations, int? row_alignment, int? max_float8_D, "
+    "int? fp8_exponent_bits, int? fp8_exponent_bias) -> Tensor"
+)
+
+_schema_lib = None
+_loaded = False
+
+
+def _op_defined() -> bool:
+    try:
+        torch._C._dispatch_find_schema_or_throw("fbgemm::" + OP_NAME, "")
+        return True
+    except RuntimeError:
+        return False
+
+
+def _define_schema() -> None:
+    global _schema_lib
+    if _op_defined():
+        return
+    _schema_lib = torch.library.Library("fbgemm", "FRAGMENT")
+    _schema_lib.define(OP_SCHEMA)
+
+
+def load_library() -> None:
+    """Define the schema (if needed) and register the HIP implementation.
+
+    Raises if the built extension is missing: there is no CPU fallback."""
+    global _loaded
+    if _loaded:
+        return
+    if not os.path.exists(TORCH_LIB) or not os.path.exists(HIP_LIB):
+        raise FileNotFoundError(
+            f"fbgemm_ascend_amd: built extension not found ({TORCH_LIB}); "
+            "run fbgemm-ascend_amd/build.py (or __graft_entry__.build()) first")
+    _define_schema()
+    torch.ops.load_library(TORCH_LIB)
+    _loaded = True
+
+
+load_library()
+
+from . import capi  # noqa: E402,F401
+from .sparse_types import PoolingMode, SparseType  # noqa: E402,F401
+from .tbe_module import IntNBitTableBatchedEmbeddingBagsCodegen  # noqa: E402,F401
+
+
+def int_nbit_split_embedding_codegen_lookup_function(**kwargs):
+    """Keyword passthrough to the registered torch op."""
+    return torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(**kwargs)

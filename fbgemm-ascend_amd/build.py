@@ -1,0 +1,72 @@
+"""In-tree build of the HIP library and its torch binding (no cmake, no JIT cache).
+
+  libtbe_hip.so    hand-written gfx950 kernels + the C ABI of include/tbe_nbit.h
+  _tbe_torch.so    registers fbgemm::int_nbit_split_embedding_codegen_lookup_function
+                   for HIP tensors; links libtbe_hip.so through $ORIGIN
+
+Both land next to this file so they travel with the source tree.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+HIP_LIB = os.path.join(PKG_DIR, "libtbe_hip.so")
+TORCH_LIB = os.path.join(PKG_DIR, "_tbe_torch.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+# hipcc flags for device code: gfx950 only, no packed-fp32 instructions.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if out.strip():
+        print(out, flush=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
+
+
+def build_hip_lib():
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
+          os.path.join(CSRC, "tbe_nbit.hip"), "-o", HIP_LIB])
+
+
+def build_torch_binding():
+    import torch
+    from torch.utils import cpp_extension
+
+    tdir = os.path.dirname(torch.__file__)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           f"-I{INCLUDE}", f"-I{ROCM}/include"]
+    for inc in cpp_extension.include_paths():
+        cmd.append(f"-I{inc}")
+    cmd += [os.path.join(CSRC, "tbe_torch.cpp"), "-o", TORCH_LIB,
+            f"-L{PKG_DIR}", "-ltbe_hip", "-Wl,-rpath,$ORIGIN",
+            f"-L{os.path.join(tdir, 'lib')}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch"]
+    _run(cmd)
+
+
+def build():
+    build_hip_lib()
+    build_torch_binding()
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

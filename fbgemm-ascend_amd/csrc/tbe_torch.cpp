@@ -1,0 +1,232 @@
+// tbe_torch.cpp — PyTorch-ROCm binding of the C ABI in include/tbe_nbit.h.
+//
+// Registers the HIP (dispatch key CUDA on PyTorch-ROCm) implementation of
+//   fbgemm::int_nbit_split_embedding_codegen_lookup_function
+// with the same argument list, checks and output allocation as the reference
+// adapter (reference: src/tbe_inference/int_nbit_split_embedding_codegen_lookup_function/
+// int_nbit_split_embedding_codegen_lookup_function.cpp, "A" below), which
+// registers the PrivateUse1 (NPU) implementation of the same schema (A:172-176).
+// The schema itself is defined by the Python loader when no fbgemm_gpu
+// provides it.
+//
+// Table metadata (weights_offsets, weights_tys, D_offsets) is planned once on
+// the host and the device copy of the plan is cached, keyed on the tensors'
+// storage and version counters: TorchRec-style modules pass the same buffers
+// every call, so after the first call no host synchronisation happens.
+#include <ATen/ATen.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <list>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "tbe_nbit.h"
+
+namespace tbe_torch {
+
+using at::Tensor;
+
+// A:37-52
+at::ScalarType sparse_type_to_scalar_type(int64_t output_dtype) {
+  switch (output_dtype) {
+    case TBE_TY_FP32: return at::kFloat;
+    case TBE_TY_FP16: return at::kHalf;
+    case TBE_TY_INT8: return at::kByte;
+    case TBE_TY_BF16: return at::kBFloat16;
+    default:
+      TORCH_CHECK(false, "Unsupported output_dtype: ", output_dtype,
+                  ". Supported: 0(FP32), 1(FP16), 2(INT8), 5(BF16)");
+  }
+}
+
+struct PlanKey {
+  const void* wo_ptr; int64_t wo_ver;
+  const void* wt_ptr; int64_t wt_ver;
+  const void* do_ptr; int64_t do_ver;
+  int64_t T, weights_bytes, row_alignment, fp8_bits, fp8_bias;
+  int device;
+  bool operator==(const PlanKey& o) const {
+    return std::tie(wo_ptr, wo_ver, wt_ptr, wt_ver, do_ptr, do_ver, T, weights_bytes, row_alignment,
+                    fp8_bits, fp8_bias, device) ==
+           std::tie(o.wo_ptr, o.wo_ver, o.wt_ptr, o.wt_ver, o.do_ptr, o.do_ver, o.T, o.weights_bytes,
+                    o.row_alignment, o.fp8_bits, o.fp8_bias, o.device);
+  }
+};
+
+struct Plan {
+  Tensor device_descs;  // uint8 [T * sizeof(TbeTableDesc)] on the weights' device
+  TbePlanSummary summary;
+};
+
+class PlanCache {
+ public:
+  Plan get(const PlanKey& key, const Tensor& weights_offsets, const Tensor& weights_tys,
+           const Tensor& D_offsets, const at::Device& dev) {
+    std::lock_guard<std::mutex> g(mu_);
+    for (auto it = entries_.begin(); it != entries_.end(); ++it) {
+      if (it->first == key) {
+        entries_.splice(entries_.begin(), entries_, it);
+        return entries_.front().second;
+      }
+    }
+    Plan p = build(key, weights_offsets, weights_tys, D_offsets, dev);
+    entries_.emplace_front(key, p);
+    if (entries_.size() > kMaxEntries) entries_.pop_back();
+    return p;
+  }
+
+ private:
+  static constexpr size_t kMaxEntries = 16;
+
+  static Plan build(const PlanKey& key, const Tensor& weights_offsets, const Tensor& weights_tys,
+                    const Tensor& D_offsets, const at::Device& dev) {
+    // one host round trip per distinct table layout
+    Tensor wo = weights_offsets.to(at::kCPU, at::kLong).contiguous();
+    Tensor wt = weights_tys.to(at::kCPU, at::kByte).contiguous();
+    Tensor dof = D_offsets.to(at::kCPU, at::kInt).contiguous();
+    TbePlanInput in{};
+    in.T = static_cast<int32_t>(key.T);
+    in.weights_offsets = wo.data_ptr<int64_t>();
+    in.weights_tys = wt.data_ptr<uint8_t>();
+    in.D_offsets = dof.data_ptr<int32_t>();
+    in.dev_weights_bytes = key.weights_bytes;
+    in.row_alignment = static_cast<int32_t>(key.row_alignment);
+    in.fp8_exponent_bits = static_cast<int32_t>(key.fp8_bits);
+    in.fp8_exponent_bias = static_cast<int32_t>(key.fp8_bias);
+    std::vector<TbeTableDesc> descs(key.T);
+    Plan p{};
+    const int rc = tbe_nbit_plan(&in, descs.data(), &p.summary);
+    TORCH_CHECK(rc == TBE_OK, "int_nbit_split_embedding_codegen_lookup_function: ", tbe_last_error());
+    Tensor host = at::empty({static_cast<int64_t>(descs.size() * sizeof(TbeTableDesc))},
+                            at::TensorOptions().dtype(at::kByte));
+    memcpy(host.data_ptr<uint8_t>(), descs.data(), descs.size() * sizeof(TbeTableDesc));
+    p.device_descs = host.to(dev);
+    return p;
+  }
+
+  std::mutex mu_;
+  std::list<std::pair<PlanKey, Plan>> entries_;
+};
+
+PlanCache& plan_cache() {
+  static PlanCache c;
+  return c;
+}
+
+// Same signature as the reference adapter (A:55-78).
+Tensor int_nbit_split_embedding_codegen_lookup_function_hip(
+    Tensor dev_weights, Tensor uvm_weights, Tensor weights_placements, Tensor weights_offsets,
+    Tensor weights_tys, Tensor D_offsets, const int64_t total_D, const int64_t max_int2_D,
+    const int64_t max_int4_D, const int64_t max_int8_D, const int64_t max_float16_D,
+    const int64_t max_float32_D, Tensor indices, Tensor offsets, const int64_t pooling_mode,
+    std::optional<Tensor> indice_weights, const int64_t output_dtype,
+    std::optional<Tensor> lxu_cache_weights, std::optional<Tensor> lxu_cache_locations,
+    const std::optional<int64_t> row_alignment, const std::optional<int64_t> max_float8_D,
+    const std::optional<int64_t> fp8_exponent_bits, const std::optional<int64_t> fp8_exponent_bias) {
+  (void)uvm_weights;
+  (void)weights_placements;
+  (void)lxu_cache_weights;
+  (void)lxu_cache_locations;
+  const c10::hip::OptionalHIPGuard guard(dev_weights.device());  // A:80
+
+  const int64_t T = weights_offsets.size(0);
+  const int64_t N = indices.numel();
+  const int64_t row_align = row_alignment.value_or(16);        // A:86
+  const int64_t fp8_bits = fp8_exponent_bits.value_or(-1);     // A:87
+  const int64_t fp8_bias = fp8_exponent_bias.value_or(-1);     // A:88
+  const int64_t max_D = std::max({max_int2_D, max_int4_D, max_int8_D, max_float8_D.value_or(0),
+                                  max_float16_D, max_float32_D});  // A:94-102
+
+  // A:104-107 and H:110-113
+  std::optional<Tensor> psw;
+  if (indice_weights && indice_weights->defined() && indice_weights->numel() > 0) {
+    psw = indice_weights->to(at::kFloat).contiguous();
+  }
+  // A:110-113: offsets follow the indices dtype
+  TORCH_CHECK(indices.scalar_type() == at::kInt || indices.scalar_type() == at::kLong,
+              "indices dtype must be int32 or int64, got ", indices.scalar_type());
+  Tensor off = offsets.scalar_type() == indices.scalar_type() ? offsets : offsets.to(indices.scalar_type());
+  off = off.contiguous();
+  Tensor idx = indices.contiguous();
+
+  // A:116-119
+  TORCH_CHECK(T > 0, "weights_offsets size must be great than 0.");
+  TORCH_CHECK(N > 0, "indices can not be empty tensor.");
+  TORCH_CHECK(off.size(0) > 1, "offsets dim_0 must be great than 1.");
+  TORCH_CHECK(weights_tys.size(0) == T, "weights_tys size must equal weights_offsets size.");
+  TORCH_CHECK(D_offsets.size(0) == T + 1, "The length of D_offsets must equal weights_offsets(", T, ") + 1.");
+  TORCH_CHECK(dev_weights.is_cuda(), "dev_weights must be a HIP device tensor");
+  TORCH_CHECK(dev_weights.scalar_type() == at::kByte, "dev_weights must be uint8");
+  TORCH_CHECK(dev_weights.is_contiguous(), "dev_weights must be contiguous");
+  TORCH_CHECK(idx.device() == dev_weights.device() && off.device() == dev_weights.device(),
+              "indices and offsets must be on the weights' device");
+  if (psw) {
+    TORCH_CHECK(psw->numel() == N, "Len mismatch: indice_weights(", psw->numel(), ") must equal indices(", N, ").");
+    TORCH_CHECK(psw->device() == dev_weights.device(), "indice_weights must be on the weights' device");
+  }
+  TORCH_CHECK(pooling_mode >= TBE_POOL_SUM && pooling_mode <= TBE_POOL_NONE, "Invalid pooling mode ",
+              pooling_mode, ": supported modes are SUM(0), MEAN(1), NONE(2)");
+  const at::ScalarType out_type = sparse_type_to_scalar_type(output_dtype);
+  TORCH_CHECK(output_dtype != TBE_TY_INT8,
+              "INT8 output_dtype is not supported (the reference kernel asserts on it as well)");
+
+  const PlanKey key{weights_offsets.data_ptr(), static_cast<int64_t>(weights_offsets._version()),
+                    weights_tys.data_ptr(),     static_cast<int64_t>(weights_tys._version()),
+                    D_offsets.data_ptr(),       static_cast<int64_t>(D_offsets._version()),
+                    T, dev_weights.numel(), row_align, fp8_bits, fp8_bias,
+                    static_cast<int>(dev_weights.get_device())};
+  const Plan plan = plan_cache().get(key, weights_offsets, weights_tys, D_offsets, dev_weights.device());
+  const TbePlanSummary& s = plan.summary;
+
+  TbeNbitArgs a{};
+  a.dev_weights = dev_weights.data_ptr<uint8_t>();
+  a.tables = reinterpret_cast<const TbeTableDesc*>(plan.device_descs.data_ptr<uint8_t>());
+  a.T = static_cast<int32_t>(T);
+  a.max_col_tiles = s.max_col_tiles;
+  a.indices = idx.data_ptr();
+  a.offsets = off.data_ptr();
+  a.index_size = static_cast<int32_t>(idx.element_size());
+  a.pooling_mode = static_cast<int32_t>(pooling_mode);
+  a.num_indices = N;
+  a.indice_weights = nullptr;
+  a.output_dtype = static_cast<int32_t>(output_dtype);
+  a.fp8_exponent_bits = static_cast<int32_t>(fp8_bits);
+  a.fp8_exponent_bias = static_cast<int32_t>(fp8_bias);
+  a.B = (off.size(0) - 1) / T;
+
+  Tensor output;
+  if (pooling_mode == TBE_POOL_NONE) {
+    // A:132-146; every table must have D == max_D (c310/README.md:96-98)
+    TORCH_CHECK(s.uniform_D && s.max_D == max_D, "nobag mode requires every table's D to equal max_D (",
+                max_D, ")");
+    output = at::empty({N, max_D}, dev_weights.options().dtype(out_type));
+    a.output_stride = max_D;
+  } else {
+    // A:148-155
+    TORCH_CHECK((off.size(0) - 1) % T == 0, "offset size = ", off.size(0),
+                " is incorrect for feature count = ", T);
+    TORCH_CHECK(s.total_D <= total_D, "D_offsets[-1] (", s.total_D, ") exceeds total_D (", total_D, ")");
+    const bool full = s.covers_output && s.total_D == total_D;
+    output = full ? at::empty({a.B, total_D}, dev_weights.options().dtype(out_type))
+                  : at::zeros({a.B, total_D}, dev_weights.options().dtype(out_type));
+    a.output_stride = total_D;
+    if (psw) a.indice_weights = psw->data_ptr<float>();
+  }
+  a.output = output.data_ptr();
+  if (output.numel() == 0) return output;
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(dev_weights.get_device()).stream();
+  const int rc = tbe_nbit_forward(&a, stream);
+  TORCH_CHECK(rc == TBE_OK, "int_nbit_split_embedding_codegen_lookup_function: ", tbe_last_error());
+  return output;
+}
+
+}  // namespace tbe_torch
+
+// PyTorch-ROCm routes HIP tensors through the CUDA dispatch key.
+TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
+  m.impl("int_nbit_split_embedding_codegen_lookup_function",
+         TORCH_FN(tbe_torch::int_nbit_split_embedding_codegen_lookup_function_hip));
+}

@@ -1,0 +1,136 @@
+"""ctypes/numpy front end of the CPU oracle (oracle/tbe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import this module, as the checker; the product path never
+does.  Semantics and citations are in the header of tbe_oracle.c; the Python
+signature mirrors torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function
+(reference A:55-78) with host numpy arrays.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libtbe_oracle.so")
+_lib = None
+
+FP32, FP16, INT8, INT4, INT2, BF16, FP8 = 0, 1, 2, 3, 4, 5, 6
+_BITS = {FP32: 32, FP16: 16, BF16: 16, INT8: 8, FP8: 8, INT4: 4, INT2: 2}
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, OpenMP)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        L.oracle_tbe_forward.restype = ctypes.c_int
+        L.oracle_tbe_forward.argtypes = [P, ctypes.c_int, P, P, P, P, P, P, ctypes.c_int, i64, i64,
+                                         ctypes.c_int, P, ctypes.c_int, i64, ctypes.c_int,
+                                         ctypes.c_int, P, P, i64, ctypes.c_int]
+        L.oracle_fp8_to_float.restype = ctypes.c_float
+        L.oracle_fp8_to_float.argtypes = [ctypes.c_uint8, ctypes.c_int, ctypes.c_int]
+        L.oracle_decode_fp8_table.argtypes = [ctypes.c_int, ctypes.c_int, P]
+        for name in ("oracle_half_to_float_n", "oracle_float_to_half_n", "oracle_float_to_bf16_n"):
+            getattr(L, name).argtypes = [P, P, i64]
+        L.oracle_row_stride.restype = i64
+        L.oracle_row_stride.argtypes = [ctypes.c_int, i64, i64]
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def row_stride(ty: int, D: int, row_alignment: int = 16) -> int:
+    return int(lib().oracle_row_stride(ty, D, row_alignment))
+
+
+def table_rows(weights_offsets, weights_tys, D_offsets, weights_bytes, row_alignment=16):
+    """Rows of each table that lie before the next table's first byte (or the buffer end)."""
+    wo = np.asarray(weights_offsets, dtype=np.int64)
+    starts = np.unique(wo)
+    rows = np.zeros(len(wo), dtype=np.int64)
+    for t in range(len(wo)):
+        nxt = starts[starts > wo[t]]
+        end = int(nxt[0]) if len(nxt) else int(weights_bytes)
+        stride = row_stride(int(weights_tys[t]), int(D_offsets[t + 1] - D_offsets[t]), row_alignment)
+        rows[t] = max(0, (end - int(wo[t])) // stride)
+    return rows
+
+
+def fp8_table(exp_bits: int, exp_bias: int) -> np.ndarray:
+    out = np.zeros(256, dtype=np.float32)
+    lib().oracle_decode_fp8_table(exp_bits, exp_bias, _ptr(out))
+    return out
+
+
+def half_to_float(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_half_to_float_n(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def float_to_half_bits(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, dtype=np.uint16)
+    lib().oracle_float_to_half_n(_ptr(f), _ptr(out), f.size)
+    return out
+
+
+def float_to_bf16_bits(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, dtype=np.uint16)
+    lib().oracle_float_to_bf16_n(_ptr(f), _ptr(out), f.size)
+    return out
+
+
+def forward(dev_weights, weights_offsets, weights_tys, D_offsets, indices, offsets,
+            pooling_mode: int, indice_weights=None, output_dtype: int = FP32,
+            row_alignment: int = 16, fp8_exponent_bits: int = -1, fp8_exponent_bias: int = -1,
+            rows=None, num_threads: int | None = None):
+    """Run the oracle.  Returns (out, out_f32): `out` holds the output dtype's bits
+    (float32 array, or uint16 array of fp16/bf16 bit patterns) and `out_f32` the fp32
+    value of every element before the final cast."""
+    w = np.ascontiguousarray(dev_weights, dtype=np.uint8)
+    wo = np.ascontiguousarray(weights_offsets, dtype=np.int64)
+    wt = np.ascontiguousarray(weights_tys, dtype=np.uint8)
+    do = np.ascontiguousarray(D_offsets, dtype=np.int32)
+    idx = np.ascontiguousarray(indices)
+    if idx.dtype not in (np.int32, np.int64):
+        raise TypeError("indices must be int32 or int64")
+    off = np.ascontiguousarray(offsets, dtype=idx.dtype)
+    T = len(wo)
+    B = (len(off) - 1) // T
+    if rows is None:
+        rows = table_rows(wo, wt, do, w.size, row_alignment)
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    psw = None if indice_weights is None else np.ascontiguousarray(indice_weights, dtype=np.float32)
+    if pooling_mode == 2:
+        max_D = int(np.max(do[1:] - do[:-1]))
+        shape = (idx.size, max_D)
+    else:
+        shape = (B, int(do[-1]))
+    out_f32 = np.zeros(shape, dtype=np.float32)
+    out = np.zeros(shape, dtype=np.float32 if output_dtype == FP32 else np.uint16)
+    nt = num_threads or os.cpu_count() or 1
+    rc = lib().oracle_tbe_forward(_ptr(w), T, _ptr(wo), _ptr(wt), _ptr(do), _ptr(rows), _ptr(idx),
+                                  _ptr(off), idx.itemsize, idx.size, B, pooling_mode, _ptr(psw),
+                                  output_dtype, row_alignment, fp8_exponent_bits, fp8_exponent_bias,
+                                  _ptr(out), _ptr(out_f32), shape[1], nt)
+    if rc != 0:
+        raise ValueError("oracle_tbe_forward rejected its arguments")
+    return out, out_f32

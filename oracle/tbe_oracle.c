@@ -1,0 +1,280 @@
+/*
+ * tbe_oracle.c — CPU restatement of the reference's quantized TBE inference
+ * forward.  TEST INFRASTRUCTURE ONLY: the GPU product never links, loads or
+ * calls this file.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg use it, as the checker (and the timed CPU baseline).
+ *
+ * Citations are relative to the reference repository root.
+ *   A = src/tbe_inference/int_nbit_split_embedding_codegen_lookup_function/
+ *       int_nbit_split_embedding_codegen_lookup_function.cpp
+ *   C = .../c310/op_kernel/common.h
+ *   P = .../c310/op_kernel/int_nbit_split_embedding_pooling_kernel.h
+ *   N = .../c310/op_kernel/int_nbit_split_embedding_nobag_kernel.h
+ *   R = .../c310/README.md
+ *
+ * The reference device kernel implements FP8 rows only (P:226-232); the
+ * INT8/INT4/INT2/FP16/FP32 row formats follow the upstream fbgemm_gpu layout
+ * that the reference's test uses as its golden (fbgemm_gpu 1.2.0, not vendored):
+ * INT rows are [fp16 scale][fp16 bias][packed codes], codes packed low bits
+ * first, row length rounded up to row_alignment bytes; value = scale*q + bias.
+ *
+ * Order of operations per bag (P:346-394, P:282-315): fp32 accumulator,
+ * rows added in index order, weighted rows as acc += w*row, MEAN multiplies by
+ * float(1)/float(L) after the last row (P:355, P:307-310), then the cast to the
+ * output dtype with round-to-nearest-even (P:330, CAST_RINT).
+ *
+ * Beyond the reference: an index outside [0, rows of its table) contributes
+ * nothing (fbgemm_gpu's pruned-row convention for -1); MEAN still divides by L.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+enum { TY_FP32 = 0, TY_FP16 = 1, TY_INT8 = 2, TY_INT4 = 3, TY_INT2 = 4, TY_BF16 = 5, TY_FP8 = 6 };
+
+static float bits_to_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static uint32_t f32_to_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+/* IEEE binary16 -> binary32, exact (every half is representable). */
+float oracle_half_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) & 1u;
+  int32_t exp = (h >> 10) & 0x1F;
+  uint32_t mant = h & 0x3FFu;
+  float mag;
+  if (exp == 0) {
+    mag = ldexpf((float)mant, -24); /* subnormal: mant * 2^-24 */
+  } else if (exp == 31) {
+    mag = mant ? NAN : INFINITY;
+  } else {
+    mag = ldexpf((float)(mant | 0x400u), exp - 25); /* (1024+mant) * 2^(exp-15-10) */
+  }
+  return sign ? -mag : mag;
+}
+
+/* binary32 -> binary16, round to nearest, ties to even. */
+uint16_t oracle_float_to_half(float f) {
+  uint32_t u = f32_to_bits(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t aexp = (u >> 23) & 0xFFu;
+  uint32_t mant = u & 0x7FFFFFu;
+  if (aexp == 0xFF) return sign | (mant ? 0x7E00u : 0x7C00u);
+  float a = fabsf(f);
+  if (a >= 65520.0f) return sign | 0x7C00u; /* rounds to infinity */
+  if (a < ldexpf(1.0f, -14)) {
+    /* subnormal half: value = k * 2^-24, k = rint(a * 2^24) (exact scaling) */
+    float k = nearbyintf(a * 16777216.0f); /* default rounding mode: ties-to-even */
+    return sign | (uint16_t)k;             /* k == 1024 becomes the smallest normal */
+  }
+  int e = (int)aexp - 127;           /* a in [2^e, 2^(e+1)), e in [-14, 15] */
+  float scaled = ldexpf(a, 10 - e);  /* in [1024, 2048), exact */
+  float k = nearbyintf(scaled);      /* ties-to-even */
+  uint32_t ki = (uint32_t)k;
+  if (ki == 2048u) { ki = 1024u; e += 1; }
+  if (e > 15) return sign | 0x7C00u;
+  return sign | (uint16_t)(((uint32_t)(e + 15) << 10) | (ki - 1024u));
+}
+
+/* binary32 -> bfloat16, round to nearest, ties to even (NaN kept quiet). */
+uint16_t oracle_float_to_bf16(float f) {
+  uint32_t u = f32_to_bits(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7FFFu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+/* FP8 code -> fp32 with exponent_bits / exponent_bias, restating C:120-167:
+ * body bits shifted into the fp32 exponent/mantissa field, multiplied by
+ * 2^(127-bias), sign OR-ed back in.  Subnormal codes (exponent field 0) are
+ * computed here as body * 2^(1-bias-m) so the result never depends on the
+ * host's handling of fp32 denormal operands. */
+float oracle_fp8_to_float(uint8_t code, int exp_bits, int exp_bias) {
+  int m = 7 - exp_bits;
+  uint32_t body = code & 0x7Fu;
+  float v;
+  if ((body >> m) == 0) {
+    v = ldexpf((float)body, 1 - exp_bias - m);
+  } else {
+    float raw = bits_to_f32(body << (exp_bits + 16)); /* C:126, C:162-163 */
+    float mult = bits_to_f32((uint32_t)(254 - exp_bias) << 23); /* C:131 */
+    v = raw * mult;                                              /* C:165 */
+  }
+  return bits_to_f32(f32_to_bits(v) | ((uint32_t)(code & 0x80u) << 24)); /* C:166 */
+}
+
+static int bits_of(int ty) {
+  switch (ty) {
+    case TY_FP32: return 32;
+    case TY_FP16: case TY_BF16: return 16;
+    case TY_INT8: case TY_FP8: return 8;
+    case TY_INT4: return 4;
+    case TY_INT2: return 2;
+    default: return 0;
+  }
+}
+
+/* Bytes of one row before padding (fbgemm_gpu layout, and P:241 for FP8). */
+int64_t oracle_unpadded_row_bytes(int ty, int64_t D) {
+  int b = bits_of(ty);
+  int64_t payload = (D * b + 7) / 8;
+  int hdr = (ty == TY_INT8 || ty == TY_INT4 || ty == TY_INT2) ? 4 : 0;
+  return payload + hdr;
+}
+
+int64_t oracle_row_stride(int ty, int64_t D, int64_t row_alignment) {
+  int64_t u = oracle_unpadded_row_bytes(ty, D);
+  return (u + row_alignment - 1) / row_alignment * row_alignment; /* P:241 */
+}
+
+/* Dequantize element d of one row. */
+static float dequant(const uint8_t* row, int ty, int64_t d, int fp8_bits, int fp8_bias) {
+  switch (ty) {
+    case TY_FP32: {
+      float v;
+      memcpy(&v, row + 4 * d, 4);
+      return v;
+    }
+    case TY_FP16: {
+      uint16_t h;
+      memcpy(&h, row + 2 * d, 2);
+      return oracle_half_to_float(h);
+    }
+    case TY_BF16: {
+      uint16_t h;
+      memcpy(&h, row + 2 * d, 2);
+      return bits_to_f32((uint32_t)h << 16);
+    }
+    case TY_FP8:
+      return oracle_fp8_to_float(row[d], fp8_bits, fp8_bias);
+    default: break;
+  }
+  uint16_t sh, bh;
+  memcpy(&sh, row, 2);
+  memcpy(&bh, row + 2, 2);
+  float scale = oracle_half_to_float(sh), bias = oracle_half_to_float(bh);
+  const uint8_t* q = row + 4;
+  uint32_t code;
+  if (ty == TY_INT8) code = q[d];
+  else if (ty == TY_INT4) code = (q[d >> 1] >> (4 * (d & 1))) & 0xFu;
+  else code = (q[d >> 2] >> (2 * (d & 3))) & 0x3u;
+  return fmaf(scale, (float)code, bias);
+}
+
+static void store_out(void* out, int out_ty, int64_t pos, float v) {
+  if (out_ty == TY_FP32) ((float*)out)[pos] = v;
+  else if (out_ty == TY_FP16) ((uint16_t*)out)[pos] = oracle_float_to_half(v);
+  else ((uint16_t*)out)[pos] = oracle_float_to_bf16(v);
+}
+
+static int64_t load_index(const void* p, int index_size, int64_t i) {
+  return index_size == 8 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
+}
+
+/*
+ * The op.  Host arrays throughout.  Returns 0, or -1 on an argument error.
+ *   table_rows[t]: rows of table t that may be addressed (indices outside are skipped).
+ *   out:     [B, total_D] (bag) or [N, max_D] (nobag) in out_ty; when out_f32 is
+ *            non-NULL the fp32 value before the cast is stored there too.
+ * Bag decomposition (P:44-85, R:40-57): bag k = t*B + b covers
+ * indices[offsets[k], offsets[k+1]) and writes out[b, D_offsets[t] : D_offsets[t+1]).
+ * Nobag (N:44-81, A:132-146): indices of table t are offsets[t*B]..offsets[(t+1)*B];
+ * out row i = dequantized row of indices[i]; columns past D stay zero.
+ */
+int oracle_tbe_forward(const uint8_t* weights, int T, const int64_t* weights_offsets,
+                       const uint8_t* weights_tys, const int32_t* D_offsets,
+                       const int64_t* table_rows, const void* indices, const void* offsets,
+                       int index_size, int64_t num_indices, int64_t B, int pooling_mode,
+                       const float* indice_weights, int out_ty, int64_t row_alignment,
+                       int fp8_bits, int fp8_bias, void* out, float* out_f32,
+                       int64_t out_stride, int num_threads) {
+  if (T <= 0 || B < 0 || row_alignment <= 0) return -1;
+  if (index_size != 4 && index_size != 8) return -1;
+  if (out_ty != TY_FP32 && out_ty != TY_FP16 && out_ty != TY_BF16) return -1;
+  if (pooling_mode < 0 || pooling_mode > 2) return -1;
+  for (int t = 0; t < T; ++t)
+    if (D_offsets[t + 1] - D_offsets[t] > 8192) return -1; /* acc_buf bound */
+  (void)num_indices;
+  if (pooling_mode == 2) {
+    for (int t = 0; t < T; ++t) {
+      int64_t lo = load_index(offsets, index_size, (int64_t)t * B);
+      int64_t hi = load_index(offsets, index_size, (int64_t)(t + 1) * B);
+      int ty = weights_tys[t];
+      int64_t D = D_offsets[t + 1] - D_offsets[t];
+      int64_t stride = oracle_row_stride(ty, D, row_alignment);
+#pragma omp parallel for schedule(static) num_threads(num_threads)
+      for (int64_t i = lo; i < hi; ++i) {
+        int64_t idx = load_index(indices, index_size, i);
+        int ok = idx >= 0 && idx < table_rows[t];
+        const uint8_t* row = weights + weights_offsets[t] + (ok ? idx : 0) * stride;
+        for (int64_t d = 0; d < out_stride; ++d) {
+          float v = (ok && d < D) ? dequant(row, ty, d, fp8_bits, fp8_bias) : 0.0f;
+          store_out(out, out_ty, i * out_stride + d, v);
+          if (out_f32) out_f32[i * out_stride + d] = v;
+        }
+      }
+    }
+    return 0;
+  }
+  int64_t nbags = (int64_t)T * B;
+#pragma omp parallel num_threads(num_threads)
+  {
+    float acc_buf[8192];
+#pragma omp for schedule(dynamic, 64)
+    for (int64_t k = 0; k < nbags; ++k) {
+      int t = (int)(k / B);
+      int64_t b = k - (int64_t)t * B;
+      int64_t start = load_index(offsets, index_size, k);
+      int64_t end = load_index(offsets, index_size, k + 1);
+      int32_t L = (int32_t)(end - start);
+      int ty = weights_tys[t];
+      int64_t D = D_offsets[t + 1] - D_offsets[t];
+      int64_t stride = oracle_row_stride(ty, D, row_alignment);
+      const uint8_t* tbase = weights + weights_offsets[t];
+      for (int64_t d = 0; d < D; ++d) acc_buf[d] = 0.0f;
+      for (int64_t i = start; i < end; ++i) {
+        int64_t idx = load_index(indices, index_size, i);
+        if (idx < 0 || idx >= table_rows[t]) continue;
+        const uint8_t* row = tbase + idx * stride;
+        if (indice_weights) {
+          float w = indice_weights[i];
+          for (int64_t d = 0; d < D; ++d)
+            acc_buf[d] = fmaf(w, dequant(row, ty, d, fp8_bits, fp8_bias), acc_buf[d]);
+        } else {
+          for (int64_t d = 0; d < D; ++d) acc_buf[d] += dequant(row, ty, d, fp8_bits, fp8_bias);
+        }
+      }
+      if (pooling_mode == 1 && L > 0) {
+        float inv = (float)1 / (float)L; /* P:355 */
+        for (int64_t d = 0; d < D; ++d) acc_buf[d] *= inv;
+      }
+      int64_t base = b * out_stride + D_offsets[t];
+      for (int64_t d = 0; d < D; ++d) {
+        store_out(out, out_ty, base + d, acc_buf[d]);
+        if (out_f32) out_f32[base + d] = acc_buf[d];
+      }
+    }
+  }
+  return 0;
+}
+
+/* Batch helpers used by the tests to pin the element decoders exhaustively. */
+void oracle_decode_fp8_table(int exp_bits, int exp_bias, float* out256) {
+  for (int c = 0; c < 256; ++c) out256[c] = oracle_fp8_to_float((uint8_t)c, exp_bits, exp_bias);
+}
+void oracle_half_to_float_n(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_half_to_float(in[i]);
+}
+void oracle_float_to_half_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_float_to_half(in[i]);
+}
+void oracle_float_to_bf16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_float_to_bf16(in[i]);
+}

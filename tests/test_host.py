@@ -1,0 +1,176 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports what
+include/tbe_nbit.h declares, the planner's layout rules and validation errors,
+the op schema registration, and the module-level packer's layout."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FP32, FP16, INT8, INT4, INT2, BF16, FP8 = 0, 1, 2, 3, 4, 5, 6
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "tbe_nbit.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(tbe_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_abi_exports_every_declared_symbol(pkg):
+    names = _header_functions()
+    assert {"tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version"} <= set(names)
+    lib = ctypes.CDLL(pkg.HIP_LIB)
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/tbe_nbit.h but not exported"
+    assert set(names) == set(pkg.capi.EXPORTS)
+
+
+def test_abi_version_and_struct_layout(pkg, tmp_path):
+    """The ctypes mirror has the C compiler's sizes and field offsets for every struct."""
+    import subprocess
+    c = pkg.capi
+    assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 1
+    structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanSummary, c.TbeNbitArgs]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tbe_nbit.h"', "int main(void){"]
+    for st in structs:
+        lines.append(f'printf("%zu\\n", sizeof({st.__name__}));')
+        for f, _ in st._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({st.__name__}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", f"-I{ROOT}/include", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()]
+    want = []
+    for st in structs:
+        want.append(ctypes.sizeof(st))
+        want += [getattr(st, f).offset for f, _ in st._fields_]
+    assert got == want
+
+
+def test_forward_rejects_bad_args_without_gpu(pkg):
+    c = pkg.capi
+    a = c.TbeNbitArgs()
+    a.T, a.B, a.index_size, a.max_col_tiles, a.output_dtype = 1, 1, 3, 1, 0
+    with pytest.raises(c.TbeError, match="int32 or int64"):
+        c.forward(a)
+    a.index_size, a.pooling_mode = 4, 7
+    with pytest.raises(c.TbeError, match="pooling mode"):
+        c.forward(a)
+    a.pooling_mode, a.output_dtype = 0, 2
+    with pytest.raises(c.TbeError, match="INT8 output"):
+        c.forward(a)
+    a.output_dtype = 9
+    with pytest.raises(c.TbeError, match="output_dtype"):
+        c.forward(a)
+    a.output_dtype, a.B = 0, 0
+    c.forward(a)  # nothing to do: returns before touching the device
+
+
+@pytest.mark.parametrize("ty,D,stride,lanes,tiles", [
+    (INT8, 128, 144, 32, 1), (INT4, 128, 80, 16, 1), (INT2, 128, 48, 8, 1), (FP16, 128, 256, 64, 1),
+    (FP32, 128, 512, 64, 2), (FP8, 128, 128, 32, 1), (BF16, 64, 128, 32, 1), (INT4, 32, 32, 4, 1),
+    (FP8, 4096, 4096, 64, 16), (INT2, 16, 16, 1, 1), (FP8, 12, 16, 4, 1)])
+def test_plan_layout(pkg, ty, D, stride, lanes, tiles):
+    descs, s = pkg.capi.plan([0], [ty], [0, D], 1000 * stride, 16, 4, 7)
+    d = descs[0]
+    assert (d.row_stride, 1 << d.log2_lanes, d.col_tiles, d.D) == (stride, lanes, tiles, D)
+    assert d.data_offset == (4 if ty in (INT8, INT4, INT2) else 0)
+    assert d.num_rows == 1000
+    assert s.max_col_tiles == tiles and s.total_D == D and s.covers_output == 1
+
+
+def test_plan_num_rows_follow_table_extents(pkg):
+    # tables laid out out of order; rows end where the next table starts
+    descs, s = pkg.capi.plan([800, 0, 400], [INT4, INT8, INT4], [0, 128, 256, 384], 1600)
+    assert [descs[i].num_rows for i in range(3)] == [10, 400 // 144, 5]
+    assert s.uniform_D == 1 and s.max_D == 128
+
+
+@pytest.mark.parametrize("kw,match", [
+    (dict(tys=[9]), "unsupported weight type"),
+    (dict(tys=[INT4], dofs=[0, 12]), "4-byte words"),
+    (dict(dofs=[0, -4]), "non-decreasing"),
+    (dict(tys=[FP8], bits=-1, bias=-1), "fp8_exponent_bits"),
+    (dict(woffs=[10 ** 9]), "outside dev_weights"),
+    (dict(align=6), "row_alignment"),
+])
+def test_plan_rejects(pkg, kw, match):
+    c = pkg.capi
+    with pytest.raises(c.TbeError, match=match):
+        c.plan(kw.get("woffs", [0]), kw.get("tys", [INT8]), kw.get("dofs", [0, 16]), 4096,
+               kw.get("align", 16), kw.get("bits", 4), kw.get("bias", 7))
+
+
+def test_plan_rejects_empty(pkg):
+    with pytest.raises(pkg.capi.TbeError, match="greater than 0"):
+        pkg.capi.plan(np.zeros(0, np.int64), np.zeros(0, np.uint8), [0], 16)
+
+
+def test_schema_registered(pkg):
+    schema = torch._C._dispatch_find_schema_or_throw(
+        "fbgemm::int_nbit_split_embedding_codegen_lookup_function", "")
+    assert schema is not None
+    s = str(torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function.default._schema)
+    for arg in ("Tensor dev_weights", "Tensor? indice_weights", "int output_dtype", "int? row_alignment",
+                "int? max_float8_D", "int? fp8_exponent_bits", "int? fp8_exponent_bias"):
+        assert arg in s
+
+
+def test_cpu_tensors_have_no_fallback(pkg):
+    from fbgemm_ascend_amd.workloads import make_workload
+    wl = make_workload(0, device="cpu", scale_rows=0.01, batch=4)
+    with pytest.raises(NotImplementedError):
+        wl.run()
+
+
+def test_module_layout_matches_oracle_rules(pkg, oracle):
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    specs = [("a", 10, 128, SparseType.INT4, 0), ("b", 7, 64, SparseType.INT8, 0),
+             ("c", 5, 32, SparseType.FP16, 0), ("d", 3, 16, SparseType.INT2, 0),
+             ("e", 4, 12, SparseType.FP8, 0)]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device="cpu")
+    strides = [oracle.row_stride(int(ty), D) for _, _, D, ty, _ in specs]
+    assert m.row_strides == strides
+    assert m.weights_offsets.tolist() == list(np.cumsum([0] + [E * s for (_, E, *_), s in zip(specs, strides)])[:-1])
+    assert m.D_offsets.tolist() == [0, 128, 192, 224, 240, 252]
+    assert (m.max_int4_D, m.max_int8_D, m.max_float16_D, m.max_int2_D, m.max_float8_D) == (128, 64, 32, 16, 12)
+    assert (m.fp8_exponent_bits, m.fp8_exponent_bias) == (4, 7)
+    m.fill_random_weights(0)
+    pay, sb = m.split_embedding_weights()[0]
+    assert pay.shape == (10, 64) and sb.shape == (10, 4)
+    sc = sb.contiguous().view(torch.float16)[:, 0].float()
+    assert bool(((sc >= 0.00099) & (sc <= 0.0101)).all())
+
+
+def test_module_quantize_roundtrip(pkg, oracle):
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    w = torch.randn(6, 32)
+    for ty, bits in ((SparseType.INT8, 8), (SparseType.INT4, 4), (SparseType.INT2, 2)):
+        m = IntNBitTableBatchedEmbeddingBagsCodegen([(6, 32, ty)], device="cpu")
+        m.load_float_weights(0, w)
+        out, _ = oracle.forward(m.weights_dev.numpy(), m.weights_offsets.numpy(), m.weights_tys.numpy(),
+                                m.D_offsets.numpy(), np.arange(6, dtype=np.int32),
+                                np.array([0, 6], np.int32), 2, None, 0)
+        step = (w.max(1).values - w.min(1).values) / ((1 << bits) - 1)
+        err = (torch.from_numpy(out) - w).abs().max(1).values
+        assert bool((err <= step * 0.5 + 2e-3 * w.abs().max()).all()), ty
+
+
+def test_workload_specs():
+    import __graft_entry__ as g
+    g.load_package()
+    from fbgemm_ascend_amd.workloads import config_spec, make_workload
+    s3 = config_spec(3)
+    assert len(s3.tables) == 64 and s3.weighted and int(s3.pooling) == 1
+    assert all(100_000 <= E <= 5_000_000 and D in (32, 64, 128, 256) for E, D, _ in s3.tables)
+    wl = make_workload(1, device="cpu", scale_rows=0.001, batch=64)
+    L = wl.lengths
+    assert int(L.min()) >= 1 and int(L.max()) <= 100 and abs(float(L.float().mean()) - 30) < 2
+    assert wl.offsets.dtype == torch.int32 and int(wl.offsets[-1]) == wl.num_indices
+    wl3 = make_workload(3, device="cpu", scale_rows=0.001, batch=32)
+    assert int(wl3.lengths.min()) == 0 and wl3.per_sample_weights is not None
