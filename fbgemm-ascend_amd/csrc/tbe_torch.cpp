@@ -14,7 +14,7 @@
 // storage and version counters: TorchRec-style modules pass the same buffers
 // every call, so after the first call no host synchronisation happens.
 #include <ATen/ATen.h>
-#include <c10/hip/HIPGuard.h>
+#include <ATen/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
@@ -130,7 +130,7 @@ Tensor int_nbit_split_embedding_codegen_lookup_function_hip(
   (void)weights_placements;
   (void)lxu_cache_weights;
   (void)lxu_cache_locations;
-  const c10::hip::OptionalHIPGuard guard(dev_weights.device());  // A:80
+  const at::OptionalDeviceGuard guard(at::device_of(dev_weights));  // A:80
 
   const int64_t T = weights_offsets.size(0);
   const int64_t N = indices.numel();
