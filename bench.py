@@ -37,6 +37,8 @@ def _parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target wall time of the CPU leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache measurement")
     ap.add_argument("--flags", type=int, default=0, help="TBE_FLAG_* tuning switches (C-ABI path)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a plain 1 GiB device copy instead (calibrates rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "tbe_int4_cfg2_traffic.json"),
                     help="HBM traffic per launch measured with rocprofv3 --pmc (JSON)")
     return ap.parse_args()
@@ -99,6 +101,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.randint(0, 255, (2 ** 30,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(),
+                          "calls": args.warmup + args.steps}), flush=True)
+        return
     wl = make_workload(args.config, device=dev)
     m = wl.module
     torch.cuda.synchronize()

@@ -12,11 +12,12 @@ import numpy as np
 
 from . import HIP_LIB
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 EXPORTS = ("tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version")
 
 TBE_OK, TBE_ERR_INVALID_ARG, TBE_ERR_UNSUPPORTED, TBE_ERR_LAUNCH = 0, -1, -2, -3
 TBE_FLAG_NO_XCD_REMAP = 0x1
+TBE_TABLE_OFFSET32 = 0x1
 
 
 class TbeTableDesc(ctypes.Structure):
@@ -25,7 +26,7 @@ class TbeTableDesc(ctypes.Structure):
                 ("row_stride", ctypes.c_int32), ("data_offset", ctypes.c_int32),
                 ("data_dwords", ctypes.c_int32), ("weight_ty", ctypes.c_uint8),
                 ("log2_lanes", ctypes.c_uint8), ("col_tiles", ctypes.c_uint8),
-                ("reserved", ctypes.c_uint8)]
+                ("flags", ctypes.c_uint8)]
 
 
 class TbePlanInput(ctypes.Structure):
@@ -35,14 +36,25 @@ class TbePlanInput(ctypes.Structure):
                 ("fp8_exponent_bits", ctypes.c_int32), ("fp8_exponent_bias", ctypes.c_int32)]
 
 
+class TbePlanGroup(ctypes.Structure):
+    _fields_ = [("weight_ty", ctypes.c_int32), ("log2_lanes", ctypes.c_int32),
+                ("offset32", ctypes.c_int32), ("first", ctypes.c_int32), ("count", ctypes.c_int32),
+                ("col_tiles", ctypes.c_int32)]
+
+
+TBE_MAX_GROUPS = 64
+
+
 class TbePlanSummary(ctypes.Structure):
     _fields_ = [("max_col_tiles", ctypes.c_int32), ("max_D", ctypes.c_int32),
                 ("total_D", ctypes.c_int32), ("uniform_D", ctypes.c_int32),
-                ("covers_output", ctypes.c_int32), ("has_fp8", ctypes.c_int32)]
+                ("covers_output", ctypes.c_int32), ("has_fp8", ctypes.c_int32),
+                ("num_groups", ctypes.c_int32), ("groups", TbePlanGroup * TBE_MAX_GROUPS)]
 
 
 class TbeNbitArgs(ctypes.Structure):
     _fields_ = [("dev_weights", ctypes.c_void_p), ("tables", ctypes.c_void_p),
+                ("table_order", ctypes.c_void_p), ("plan", ctypes.POINTER(TbePlanSummary)),
                 ("T", ctypes.c_int32), ("max_col_tiles", ctypes.c_int32), ("B", ctypes.c_int64),
                 ("indices", ctypes.c_void_p), ("offsets", ctypes.c_void_p),
                 ("index_size", ctypes.c_int32), ("pooling_mode", ctypes.c_int32),
@@ -64,7 +76,7 @@ def lib():
         L = ctypes.CDLL(HIP_LIB)
         L.tbe_nbit_plan.restype = ctypes.c_int
         L.tbe_nbit_plan.argtypes = [ctypes.POINTER(TbePlanInput), ctypes.POINTER(TbeTableDesc),
-                                    ctypes.POINTER(TbePlanSummary)]
+                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(TbePlanSummary)]
         L.tbe_nbit_forward.restype = ctypes.c_int
         L.tbe_nbit_forward.argtypes = [ctypes.POINTER(TbeNbitArgs), ctypes.c_void_p]
         L.tbe_last_error.restype = ctypes.c_char_p
@@ -87,7 +99,8 @@ def last_error() -> str:
 
 def plan(weights_offsets, weights_tys, D_offsets, dev_weights_bytes: int, row_alignment: int = 16,
          fp8_exponent_bits: int = -1, fp8_exponent_bias: int = -1):
-    """Host planner.  Returns (descs: ctypes array of TbeTableDesc, summary)."""
+    """Host planner.  Returns (descs: ctypes array of TbeTableDesc, order: int32 numpy
+    array, summary: TbePlanSummary)."""
     wo = np.ascontiguousarray(weights_offsets, dtype=np.int64)
     wt = np.ascontiguousarray(weights_tys, dtype=np.uint8)
     do = np.ascontiguousarray(D_offsets, dtype=np.int32)
@@ -95,11 +108,13 @@ def plan(weights_offsets, weights_tys, D_offsets, dev_weights_bytes: int, row_al
     inp = TbePlanInput(T, wo.ctypes.data, wt.ctypes.data, do.ctypes.data, int(dev_weights_bytes),
                        int(row_alignment), int(fp8_exponent_bits), int(fp8_exponent_bias))
     descs = (TbeTableDesc * max(T, 1))()
+    order = np.zeros(max(T, 1), dtype=np.int32)
     summary = TbePlanSummary()
-    rc = lib().tbe_nbit_plan(ctypes.byref(inp), descs, ctypes.byref(summary))
+    rc = lib().tbe_nbit_plan(ctypes.byref(inp), descs,
+                             order.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(summary))
     if rc != TBE_OK:
         raise TbeError(rc, last_error())
-    return descs, summary
+    return descs, order[:T], summary
 
 
 def descs_to_bytes(descs) -> bytes:
@@ -124,11 +139,11 @@ def forward_tensors(dev_weights, weights_offsets, weights_tys, D_offsets, indice
     wo = weights_offsets.detach().cpu().numpy()
     wt = weights_tys.detach().cpu().numpy()
     do = D_offsets.detach().cpu().numpy()
-    descs, s = plan(wo, wt, do, dev_weights.numel(), row_alignment, fp8_exponent_bits,
-                    fp8_exponent_bias)
+    descs, order, s = plan(wo, wt, do, dev_weights.numel(), row_alignment, fp8_exponent_bits,
+                           fp8_exponent_bias)
     dev = dev_weights.device
-    raw = np.frombuffer(descs_to_bytes(descs), dtype=np.uint8).copy()
-    tables = torch.from_numpy(raw).to(dev)
+    tables = torch.from_numpy(np.frombuffer(descs_to_bytes(descs), dtype=np.uint8).copy()).to(dev)
+    order_d = torch.from_numpy(order.copy()).to(dev)
     T = int(wo.size)
     B = (offsets.numel() - 1) // T
     out_dt = {0: torch.float32, 1: torch.float16, 5: torch.bfloat16}.get(int(output_dtype), torch.uint8)
@@ -138,6 +153,8 @@ def forward_tensors(dev_weights, weights_offsets, weights_tys, D_offsets, indice
     a = TbeNbitArgs()
     a.dev_weights = dev_weights.data_ptr()
     a.tables = tables.data_ptr()
+    a.table_order = order_d.data_ptr()
+    a.plan = ctypes.pointer(s)
     a.T = T
     a.max_col_tiles = s.max_col_tiles
     a.B = B
@@ -155,5 +172,5 @@ def forward_tensors(dev_weights, weights_offsets, weights_tys, D_offsets, indice
     a.output_stride = out.shape[1]
     stream = torch.cuda.current_stream(dev).cuda_stream
     forward(a, stream)
-    out._tbe_keepalive = tables  # the descriptor array must outlive the async launch
+    out._tbe_keepalive = (tables, order_d)  # the plan arrays must outlive the async launch
     return out

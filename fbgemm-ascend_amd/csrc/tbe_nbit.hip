@@ -11,33 +11,44 @@
 // Design (MI355X-first, not a port of the AscendC kernels):
 //  * The path is an HBM-bound gather-reduce: no MFMA.  A work item is one bag
 //    (table t, sample b) and, for rows wider than 256 bytes, one 256-byte column
-//    tile of it; one 64-wide wavefront owns one item.  Launching one wave per
-//    item lets the hardware dispatcher balance Poisson/Zipf bag lengths; the
-//    reference instead splits bags statically by count over cores (P:119-131).
-//  * A row's payload is split over G = 2^log2_lanes lanes, one 4-byte word per
-//    lane, so one vector load instruction fetches R = 64/G rows; kUnroll such
-//    loads are issued before any is consumed to keep many rows in flight.
-//  * The bag's indices are staged 64 at a time with one coalesced load and
-//    handed to the lanes that gather each row through the LDS crossbar
-//    (ds_bpermute), so no lane re-reads an index.
-//  * Dequantization is fused: INT rows carry an fp16 scale/bias header; each
-//    lane accumulates scale*q per element and the bias once per row (summed
-//    into the element at the end), so a code costs one convert and one FMA.
-//  * Partial sums of the R row slots are reduced across the wavefront with
-//    xor shuffles; slot 0 writes the D-wide output slice with vector stores.
-//  * Blocks are renumbered so consecutive bags (which share a table) stay on
-//    one XCD: each XCD's private L2 then caches the hot rows of a few tables
-//    instead of all of them.
+//    tile of it; one 64-wide wavefront pools one item at a time.
+//  * The host planner groups tables by (weight type, lanes per row).  Each group
+//    launches a kernel compiled for exactly that shape, so the register budget
+//    (and with it the number of resident waves) is that of one row format, not
+//    of the worst one.  Kernels are persistent: the grid holds what the GPU keeps
+//    resident and each wave walks items.
+//  * Items of a group are split into one contiguous range per XCD (the hardware
+//    places block i on XCD i % 8); the waves of an XCD interleave over its range.
+//    Bags of one table are adjacent, so each XCD's L2 caches the hot rows of
+//    about 1/8 of the tables instead of all of them.
+//  * A row's payload is split over G = 2^LG lanes, one 4-byte word per lane, so
+//    one load instruction fetches R = 64/G rows.  The bag's indices are staged 64
+//    at a time with one coalesced load, each lane turns its index into a byte
+//    offset, and the lanes that gather a row fetch that offset through the LDS
+//    crossbar (ds_bpermute).  All row loads of a step are issued before any is
+//    consumed; rows are read with buffer loads at 32-bit offsets from the table
+//    base, and slots past the bag or rejected indices use an offset that fails
+//    the buffer range check, which returns zero.  The load phase is therefore
+//    straight-line code.
+//  * Dequantization is fused: an INT code q is fed to v_fma_mix_f32 as the fp16
+//    subnormal q*2^-24 (the code bits are the operand, no convert), multiplied by
+//    the row's fp16 scale, accumulated in fp32; the bias is summed once per row.
+//    Scaling by 2^24 at the end is exact, so the result is the plain fp32 sum.
+//  * Partial sums of the R row slots are reduced with v_permlane32_swap /
+//    v_permlane16_swap and DPP row rotations; slot 0 writes the output slice.
 #include <hip/hip_runtime.h>
 
+#include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "tbe_nbit.h"
@@ -47,34 +58,125 @@ namespace tbe {
 constexpr int kWave = 64;
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = kWave * kWavesPerBlock;
-constexpr int kUnroll = 8;
 constexpr int kNumXcd = 8;
+constexpr int kUnrollWide = 8;
+
+// Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle).
+constexpr int kRsrcWord3 = 0x00020000;
+// Offset that fails the buffer range check, so the load returns zero (rows past
+// the bag, rejected indices).  Row offsets of 32-bit tables stay below 2^31.
+constexpr uint32_t kNoRow = 0x80000000u;
+
+// Unsigned division by a runtime-invariant divisor with one multiply-high
+// (Granlund & Montgomery, PLDI 1994): q = (mulhi(n, mul) + n) >> shift,
+// exact for n < 2^31.
+struct FastDiv {
+  uint32_t d, mul, shift;
+};
 
 struct Fp8Consts {
   uint32_t shift;      // exponent_bits + 16: body bits -> fp32 exponent/mantissa field (C:126)
   uint32_t mant_bits;  // 7 - exponent_bits
   float mult;          // 2^(127 - bias) (C:131)
   float sub_scale;     // 2^(1 - bias - mant_bits): value of one unit of a subnormal body
+  uint32_t h16_shift;  // exponent_bits + 3: body bits -> fp16 exponent/mantissa field
+  float h16_scale;     // 2^(15 - bias): fp16 reading of the placed body -> code value
+  int32_t h16_ok;      // exponent_bits <= 4: every body fits a finite fp16
 };
 
 struct KParams {
   const uint8_t* __restrict__ weights;
   const TbeTableDesc* __restrict__ tables;
+  const int32_t* __restrict__ order;  // group's table ids: order[group_first + i]
   const void* __restrict__ indices;
   const void* __restrict__ offsets;
   const float* __restrict__ psw;
   void* __restrict__ out;
   int64_t out_stride;
-  int64_t B;
-  int64_t num_items;
   int64_t num_indices;
+  int32_t B;
   int32_t T;
-  int32_t col_tiles;
-  int32_t xcd_remap;
-  int32_t num_blocks;
+  int32_t group_first;
+  int32_t group_count;
+  int32_t col_tiles;    // of the group
+  int32_t num_items;    // group_count * B * col_tiles (bag modes), index chunks (nobag)
+  int32_t index64;
+  int32_t out_ty;
   int32_t mean;
+  int32_t xcd;
+  FastDiv div_B;
+  FastDiv div_tiles;
   Fp8Consts fp8;
 };
+
+// ---------------------------------------------------------------- small helpers
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  const uint64_t hi = (static_cast<uint64_t>(n) * f.mul) >> 32;
+  return static_cast<uint32_t>((hi + n) >> f.shift);
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Generic pointer -> constant address space, so loads at wave-uniform addresses
+// become scalar loads (device pass only; the host pass of hipcc parses device
+// functions but never emits them).
+#if defined(__HIP_DEVICE_COMPILE__)
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* as_constant(const T* p) {
+  return (const __attribute__((address_space(4))) T*)(p);
+}
+#else
+template <typename T>
+__device__ __forceinline__ const T* as_constant(const T* p) { return p; }
+#endif
+
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* ptr) {
+  return *as_constant(ptr);
+}
+
+struct DescWords {
+  uint32_t w[sizeof(TbeTableDesc) / 4];
+};
+static_assert(sizeof(TbeTableDesc) == 40, "TbeTableDesc layout");
+
+// Table descriptor at a wave-uniform address, read as dwords and kept in SGPRs.
+__device__ __forceinline__ TbeTableDesc load_desc(const TbeTableDesc* ptr) {
+  DescWords x = *as_constant(reinterpret_cast<const DescWords*>(ptr));
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(sizeof(TbeTableDesc) / 4); ++i)
+    x.w[i] = static_cast<uint32_t>(uniform(static_cast<int>(x.w[i])));
+  TbeTableDesc d;
+  d.weights_offset = static_cast<int64_t>(x.w[0] | (static_cast<uint64_t>(x.w[1]) << 32));
+  d.num_rows = static_cast<int64_t>(x.w[2] | (static_cast<uint64_t>(x.w[3]) << 32));
+  d.D = static_cast<int32_t>(x.w[4]);
+  d.D_offset = static_cast<int32_t>(x.w[5]);
+  d.row_stride = static_cast<int32_t>(x.w[6]);
+  d.data_offset = static_cast<int32_t>(x.w[7]);
+  d.data_dwords = static_cast<int32_t>(x.w[8]);
+  d.weight_ty = static_cast<uint8_t>(x.w[9]);
+  d.log2_lanes = static_cast<uint8_t>(x.w[9] >> 8);
+  d.col_tiles = static_cast<uint8_t>(x.w[9] >> 16);
+  d.flags = static_cast<uint8_t>(x.w[9] >> 24);
+  return d;
+}
+
+// Entry i of the indices / offsets array (int32 or int64), any address.
+__device__ __forceinline__ int64_t load_index(const KParams& p, const void* base, int64_t i) {
+  return p.index64 ? static_cast<const int64_t*>(base)[i]
+                   : static_cast<int64_t>(static_cast<const int32_t*>(base)[i]);
+}
+
+// Entry i of the offsets array at a wave-uniform position (scalar load).
+__device__ __forceinline__ int64_t load_offset(const KParams& p, int64_t i) {
+  return p.index64 ? load_uniform(static_cast<const int64_t*>(p.offsets) + i)
+                   : static_cast<int64_t>(load_uniform(static_cast<const int32_t*>(p.offsets) + i));
+}
+
+__device__ __forceinline__ uint32_t load_word(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
 
 // ---------------------------------------------------------------- element decode
 
@@ -87,14 +189,12 @@ template <> struct Traits<TBE_TY_INT8> { static constexpr int kEpd = 4;  static 
 template <> struct Traits<TBE_TY_INT4> { static constexpr int kEpd = 8;  static constexpr bool kHdr = true; };
 template <> struct Traits<TBE_TY_INT2> { static constexpr int kEpd = 16; static constexpr bool kHdr = true; };
 
-__device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
+// Halves of a word read as fp16 (the backend folds these into v_fma_mix_f32 operands).
+__device__ __forceinline__ float h16lo(uint32_t x) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x & 0xFFFFu)));
 }
-
-// byte k of x as float (the backend selects v_cvt_f32_ubyte{k})
-template <int k>
-__device__ __forceinline__ float ubyte_f(uint32_t x) {
-  return static_cast<float>((x >> (8 * k)) & 0xFFu);
+__device__ __forceinline__ float h16hi(uint32_t x) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> 16)));
 }
 
 __device__ __forceinline__ float fp8_decode(uint32_t code, const Fp8Consts& c) {
@@ -108,43 +208,109 @@ __device__ __forceinline__ float fp8_decode(uint32_t code, const Fp8Consts& c) {
   return __uint_as_float(__float_as_uint(v) | ((code & 0x80u) << 24));
 }
 
+// Exact element values of one payload word (scale/bias not applied).
 template <int WT>
 __device__ __forceinline__ void decode(uint32_t d, float (&v)[Traits<WT>::kEpd], const Fp8Consts& c) {
   if constexpr (WT == TBE_TY_FP32) {
     v[0] = __uint_as_float(d);
   } else if constexpr (WT == TBE_TY_FP16) {
-    v[0] = half_bits_to_float(d & 0xFFFFu);
-    v[1] = half_bits_to_float(d >> 16);
+    v[0] = h16lo(d);
+    v[1] = h16hi(d);
   } else if constexpr (WT == TBE_TY_BF16) {
     v[0] = __uint_as_float(d << 16);
     v[1] = __uint_as_float(d & 0xFFFF0000u);
   } else if constexpr (WT == TBE_TY_FP8) {
-    v[0] = fp8_decode(d & 0xFFu, c);
-    v[1] = fp8_decode((d >> 8) & 0xFFu, c);
-    v[2] = fp8_decode((d >> 16) & 0xFFu, c);
-    v[3] = fp8_decode(d >> 24, c);
-  } else if constexpr (WT == TBE_TY_INT8) {
-    v[0] = ubyte_f<0>(d);
-    v[1] = ubyte_f<1>(d);
-    v[2] = ubyte_f<2>(d);
-    v[3] = ubyte_f<3>(d);
-  } else if constexpr (WT == TBE_TY_INT4) {
-    // byte b holds element 2b in its low nibble and 2b+1 in its high nibble
-    const uint32_t lo = d & 0x0F0F0F0Fu;
-    const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;
-    v[0] = ubyte_f<0>(lo); v[1] = ubyte_f<0>(hi);
-    v[2] = ubyte_f<1>(lo); v[3] = ubyte_f<1>(hi);
-    v[4] = ubyte_f<2>(lo); v[5] = ubyte_f<2>(hi);
-    v[6] = ubyte_f<3>(lo); v[7] = ubyte_f<3>(hi);
-  } else {  // INT2: byte b holds elements 4b..4b+3, bits 1:0 first
-    const uint32_t m0 = d & 0x03030303u;
-    const uint32_t m1 = (d >> 2) & 0x03030303u;
-    const uint32_t m2 = (d >> 4) & 0x03030303u;
-    const uint32_t m3 = (d >> 6) & 0x03030303u;
-    v[0] = ubyte_f<0>(m0);  v[1] = ubyte_f<0>(m1);  v[2] = ubyte_f<0>(m2);  v[3] = ubyte_f<0>(m3);
-    v[4] = ubyte_f<1>(m0);  v[5] = ubyte_f<1>(m1);  v[6] = ubyte_f<1>(m2);  v[7] = ubyte_f<1>(m3);
-    v[8] = ubyte_f<2>(m0);  v[9] = ubyte_f<2>(m1);  v[10] = ubyte_f<2>(m2); v[11] = ubyte_f<2>(m3);
-    v[12] = ubyte_f<3>(m0); v[13] = ubyte_f<3>(m1); v[14] = ubyte_f<3>(m2); v[15] = ubyte_f<3>(m3);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = fp8_decode((d >> (8 * e)) & 0xFFu, c);
+  } else {
+    // INT8/INT4/INT2: element e sits at bits [e*bits, (e+1)*bits), low bits first
+    constexpr int bits = 32 / Traits<WT>::kEpd;
+#pragma unroll
+    for (int e = 0; e < Traits<WT>::kEpd; ++e) v[e] = static_cast<float>((d >> (bits * e)) & ((1u << bits) - 1));
+  }
+}
+
+// ---------------------------------------------------------------- fused dequant + accumulate
+
+// Factor applied to the element accumulators after the last row.  INT codes q are
+// accumulated as the fp16 subnormal q * 2^-24 (the code itself is the bit pattern,
+// so no conversion instruction is needed and every product is exact in fp32);
+// scaling by a power of two commutes with rounding, so the result equals the
+// plain fp32 sum of scale*q.
+template <int WT>
+__device__ __forceinline__ constexpr float acc_post_scale() {
+  return (WT == TBE_TY_INT8 || WT == TBE_TY_INT4 || WT == TBE_TY_INT2) ? 16777216.0f : 1.0f;
+}
+
+// Add one row's contribution: acc[e] += w * value[e] (value = scale*q + bias for INT
+// rows: the scale part goes to acc, the bias to bacc once per row).
+// `d` is the lane's payload word, `h` the row's header word (INT rows).
+template <int WT, bool WEIGHTED>
+__device__ __forceinline__ void accum_row(float (&acc)[Traits<WT>::kEpd], float& bacc, uint32_t d,
+                                          uint32_t h, float w, const Fp8Consts& c) {
+  constexpr int E = Traits<WT>::kEpd;
+  if constexpr (Traits<WT>::kHdr) {
+    float s = h16lo(h);
+    float bi = h16hi(h);
+    if constexpr (WEIGHTED) {
+      s *= w;
+      bi *= w;
+    }
+    bacc += bi;
+    if constexpr (WT == TBE_TY_INT8) {
+      // halves of p0 hold bytes 0 and 2, of p1 bytes 1 and 3
+      const uint32_t p0 = d & 0x00FF00FFu, p1 = (d >> 8) & 0x00FF00FFu;
+      acc[0] = fmaf(h16lo(p0), s, acc[0]);
+      acc[2] = fmaf(h16hi(p0), s, acc[2]);
+      acc[1] = fmaf(h16lo(p1), s, acc[1]);
+      acc[3] = fmaf(h16hi(p1), s, acc[3]);
+    } else if constexpr (WT == TBE_TY_INT4) {
+      // nibbles j and j+4 of the word are elements j and j+4
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t pj = (d >> (4 * j)) & 0x000F000Fu;
+        acc[j] = fmaf(h16lo(pj), s, acc[j]);
+        acc[j + 4] = fmaf(h16hi(pj), s, acc[j + 4]);
+      }
+    } else {  // INT2: 2-bit fields j and j+8 are elements j and j+8
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t pj = (d >> (2 * j)) & 0x00030003u;
+        acc[j] = fmaf(h16lo(pj), s, acc[j]);
+        acc[j + 8] = fmaf(h16hi(pj), s, acc[j + 8]);
+      }
+    }
+  } else if constexpr (WT == TBE_TY_FP16) {
+    if constexpr (WEIGHTED) {
+      acc[0] = fmaf(h16lo(d), w, acc[0]);
+      acc[1] = fmaf(h16hi(d), w, acc[1]);
+    } else {
+      acc[0] += h16lo(d);
+      acc[1] += h16hi(d);
+    }
+  } else if constexpr (WT == TBE_TY_FP8) {
+    if (c.h16_ok) {
+      // place each 7-bit body into an fp16 exponent/mantissa field, sign to bit 15:
+      // fp16 value * 2^(15-bias) is the code's value (subnormal codes included)
+      const float m = WEIGHTED ? c.h16_scale * w : c.h16_scale;
+      const uint32_t x0 = d & 0x00FF00FFu, x1 = (d >> 8) & 0x00FF00FFu;
+      const uint32_t p0 = ((x0 & 0x007F007Fu) << c.h16_shift) | ((x0 & 0x00800080u) << 8);
+      const uint32_t p1 = ((x1 & 0x007F007Fu) << c.h16_shift) | ((x1 & 0x00800080u) << 8);
+      acc[0] = fmaf(h16lo(p0), m, acc[0]);
+      acc[2] = fmaf(h16hi(p0), m, acc[2]);
+      acc[1] = fmaf(h16lo(p1), m, acc[1]);
+      acc[3] = fmaf(h16hi(p1), m, acc[3]);
+    } else {
+      float v[E];
+      decode<WT>(d, v, c);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = WEIGHTED ? fmaf(v[e], w, acc[e]) : acc[e] + v[e];
+    }
+  } else {  // FP32, BF16
+    float v[E];
+    decode<WT>(d, v, c);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = WEIGHTED ? fmaf(v[e], w, acc[e]) : acc[e] + v[e];
   }
 }
 
@@ -157,102 +323,225 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-struct Bf16Out { uint16_t bits; };
+template <int E>
+__device__ __forceinline__ void store_f32(float* o, const float (&r)[E]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(o);
+  if constexpr (E % 4 == 0) {
+    if ((a & 15u) == 0) {
+#pragma unroll
+      for (int i = 0; i < E; i += 4)
+        *reinterpret_cast<float4*>(o + i) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
+      return;
+    }
+  }
+  if constexpr (E % 2 == 0) {
+    if ((a & 7u) == 0) {
+#pragma unroll
+      for (int i = 0; i < E; i += 2) *reinterpret_cast<float2*>(o + i) = make_float2(r[i], r[i + 1]);
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < E; ++i) o[i] = r[i];
+}
 
-template <typename OutT, int E>
-__device__ __forceinline__ void store_slice(OutT* dst, const float (&r)[E]) {
-  if constexpr (sizeof(OutT) == 4) {
-    float* o = reinterpret_cast<float*>(dst);
-    const uintptr_t a = reinterpret_cast<uintptr_t>(o);
-    if constexpr (E % 4 == 0) {
-      if ((a & 15u) == 0) {
+template <int E>
+__device__ __forceinline__ void store_b16(uint16_t* o, const uint16_t (&b)[E]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(o);
+  if constexpr (E % 8 == 0) {
+    if ((a & 15u) == 0) {
 #pragma unroll
-        for (int i = 0; i < E; i += 4)
-          *reinterpret_cast<float4*>(o + i) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
-        return;
+      for (int i = 0; i < E; i += 8) {
+        uint4 w;
+        w.x = b[i] | (uint32_t(b[i + 1]) << 16);
+        w.y = b[i + 2] | (uint32_t(b[i + 3]) << 16);
+        w.z = b[i + 4] | (uint32_t(b[i + 5]) << 16);
+        w.w = b[i + 6] | (uint32_t(b[i + 7]) << 16);
+        *reinterpret_cast<uint4*>(o + i) = w;
       }
+      return;
     }
-    if constexpr (E % 2 == 0) {
-      if ((a & 7u) == 0) {
+  }
+  if constexpr (E % 4 == 0) {
+    if ((a & 7u) == 0) {
 #pragma unroll
-        for (int i = 0; i < E; i += 2) *reinterpret_cast<float2*>(o + i) = make_float2(r[i], r[i + 1]);
-        return;
+      for (int i = 0; i < E; i += 4) {
+        uint2 w;
+        w.x = b[i] | (uint32_t(b[i + 1]) << 16);
+        w.y = b[i + 2] | (uint32_t(b[i + 3]) << 16);
+        *reinterpret_cast<uint2*>(o + i) = w;
       }
+      return;
     }
+  }
+  if constexpr (E % 2 == 0) {
+    if ((a & 3u) == 0) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) o[i] = r[i];
+      for (int i = 0; i < E; i += 2)
+        *reinterpret_cast<uint32_t*>(o + i) = b[i] | (uint32_t(b[i + 1]) << 16);
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < E; ++i) o[i] = b[i];
+}
+
+// Write E consecutive output elements starting at element `pos` of the output,
+// converting to the output dtype (fp16 / bf16 round to nearest even, P:330).
+template <int E>
+__device__ __forceinline__ void store_out(const KParams& p, int64_t pos, const float (&r)[E]) {
+  if (p.out_ty == TBE_TY_FP32) {
+    store_f32<E>(static_cast<float*>(p.out) + pos, r);
   } else {
     uint16_t b[E];
+    if (p.out_ty == TBE_TY_FP16) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      if constexpr (std::is_same<OutT, Bf16Out>::value) {
-        b[i] = static_cast<uint16_t>(f32_to_bf16_bits(r[i]));
-      } else {
-        b[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(r[i]));  // RNE
-      }
+      for (int i = 0; i < E; ++i) b[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(r[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) b[i] = static_cast<uint16_t>(f32_to_bf16_bits(r[i]));
     }
-    uint16_t* o = reinterpret_cast<uint16_t*>(dst);
-    const uintptr_t a = reinterpret_cast<uintptr_t>(o);
-    if constexpr (E % 8 == 0) {
-      if ((a & 15u) == 0) {
-#pragma unroll
-        for (int i = 0; i < E; i += 8) {
-          uint4 w;
-          w.x = b[i] | (uint32_t(b[i + 1]) << 16);
-          w.y = b[i + 2] | (uint32_t(b[i + 3]) << 16);
-          w.z = b[i + 4] | (uint32_t(b[i + 5]) << 16);
-          w.w = b[i + 6] | (uint32_t(b[i + 7]) << 16);
-          *reinterpret_cast<uint4*>(o + i) = w;
-        }
-        return;
-      }
-    }
-    if constexpr (E % 4 == 0) {
-      if ((a & 7u) == 0) {
-#pragma unroll
-        for (int i = 0; i < E; i += 4) {
-          uint2 w;
-          w.x = b[i] | (uint32_t(b[i + 1]) << 16);
-          w.y = b[i + 2] | (uint32_t(b[i + 3]) << 16);
-          *reinterpret_cast<uint2*>(o + i) = w;
-        }
-        return;
-      }
-    }
-    if constexpr (E % 2 == 0) {
-      if ((a & 3u) == 0) {
-#pragma unroll
-        for (int i = 0; i < E; i += 2)
-          *reinterpret_cast<uint32_t*>(o + i) = b[i] | (uint32_t(b[i + 1]) << 16);
-        return;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < E; ++i) o[i] = b[i];
+    store_b16<E>(static_cast<uint16_t*>(p.out) + pos, b);
   }
 }
 
-__device__ __forceinline__ uint32_t load_word(const uint8_t* p) {
-  return *reinterpret_cast<const uint32_t*>(p);
+// ---------------------------------------------------------------- cross-lane sums
+
+__device__ __forceinline__ float sum_xor32(float v) {
+  // v_permlane32_swap exchanges the two 32-lane halves; adding both results
+  // gives every lane v[l] + v[l ^ 32]
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Block renumbering: hardware hands block i to XCD i % 8; give XCD x a contiguous
-// run of logical blocks so the bags it pools come from few tables.
-__device__ __forceinline__ int remap_block(int bid, int nblk) {
-  const int q = nblk / kNumXcd, r = nblk % kNumXcd;
-  const int xcd = bid % kNumXcd, local = bid / kNumXcd;
-  return (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+// v[l] + v[(l + n) mod 16 within the lane's row of 16]; applied for n = 8,4,2,1 in
+// that order it sums lanes that differ in the low bits
+template <int n>
+__device__ __forceinline__ float add_row_ror(float v) {
+  const int r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + n, 0xF, 0xF, false);
+  return v + __int_as_float(r);
+}
 
-// ---------------------------------------------------------------- pooled (SUM / MEAN)
+__device__ __forceinline__ float sum_slots(float v, int lg) {
+  if (lg <= 5) v = sum_xor32(v);
+  if (lg <= 4) v = sum_xor16(v);
+  if (lg <= 3) v = add_row_ror<8>(v);
+  if (lg <= 2) v = add_row_ror<4>(v);
+  if (lg <= 1) v = add_row_ror<2>(v);
+  if (lg == 0) v = add_row_ror<1>(v);
+  return v;
+}
 
-// One wavefront pools one bag [start, start+L) of table `td` over column tile `ct`.
-// P:44-85 (bag walk), P:282-315 (pooling), P:346-394 (chunked bag), P:319-342 (cast/store).
-template <int WT, typename IndexT, typename OutT, bool WEIGHTED>
-__device__ __forceinline__ void pool_bag(const KParams& p, const TbeTableDesc& td, int64_t start,
-                                         int L, int ct, int64_t b) {
+// Sum over the row slots: lanes that agree in bits [0, lg) and differ above.
+template <int E, bool HDR>
+__device__ __forceinline__ void reduce_slots(float (&acc)[E], float& bacc, int lg) {
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = sum_slots(acc[e], lg);
+  if (HDR) bacc = sum_slots(bacc, lg);
+}
+
+// Final value of the lane's E elements and their store (slot 0 lanes only).
+template <int WT>
+__device__ __forceinline__ void finish_bag(const KParams& p, const TbeTableDesc& td, int L, int dw, int64_t b,
+                                           const float (&acc)[Traits<WT>::kEpd], float bacc) {
+  constexpr int E = Traits<WT>::kEpd;
+  const float scale = (p.mean && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;  // P:355
+  float r[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float x = Traits<WT>::kHdr ? fmaf(acc[e], acc_post_scale<WT>(), bacc) : acc[e];
+    r[e] = p.mean ? x * scale : x;
+  }
+  store_out<E>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E, r);
+}
+
+// ---------------------------------------------------------------- pooled bag, 32-bit tables
+
+// Steps (of R = 64 >> LG rows each) whose loads are issued back to back before
+// any is consumed: 16-32 rows in flight per wave for wide rows, a whole 64-index
+// chunk for short rows.
+template <int LG>
+constexpr int unroll_for() {
+  return LG >= 5 ? 16 : (LG == 4 ? 8 : kWave / (kWave >> LG));
+}
+
+// One wavefront pools bag [start, start+L) of table `td` over column tile `ct`
+// (P:44-85 bag walk, P:282-315 pooling, P:346-394 chunked bag, P:319-342 store)
+// for a table whose rows span < 2 GiB.
+template <int WT, int LG, bool WEIGHTED>
+__device__ __forceinline__ void pool_bag_fast(const KParams& p, const TbeTableDesc& td, int64_t start, int L,
+                                              int ct, int64_t b) {
+  constexpr int E = Traits<WT>::kEpd;
+  constexpr bool HDR = Traits<WT>::kHdr;
+  constexpr int R = kWave >> LG;
+  constexpr int U = unroll_for<LG>();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int slot = lane >> LG;
+  const int dw = ct * kWave + (lane & ((1 << LG) - 1));
+  const bool col_ok = dw < td.data_dwords;
+  const uint32_t col = static_cast<uint32_t>(td.data_offset + (col_ok ? 4 * dw : 0));
+  const uint32_t rows = static_cast<uint32_t>(td.num_rows);
+  const uint32_t stride = static_cast<uint32_t>(td.row_stride);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.weights + td.weights_offset), 0, static_cast<int>(rows * stride), kRsrcWord3);
+  const int slot4 = slot * 4;
+
+  float acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  float bacc = 0.f;
+
+  for (int base = 0; base < L; base += kWave) {
+    const int n = min(kWave, L - base);
+    // stage up to 64 indices of the bag with one coalesced load; each lane turns
+    // its index into a byte offset once
+    uint32_t my_off = kNoRow;
+    float my_w = 0.f;
+    if (lane < n) {
+      const int64_t idx = load_index(p, p.indices, start + base + lane);
+      if (static_cast<uint64_t>(idx) < rows) my_off = static_cast<uint32_t>(idx) * stride;
+      if constexpr (WEIGHTED) my_w = p.psw[start + base + lane];
+    }
+    for (int r0 = 0; r0 < n; r0 += R * U) {
+      uint32_t d[U], h[U];
+      float w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool live = r0 + u * R < n;  // wave-uniform
+        // slot r0+u*R+slot < 64 whenever live (R divides 64 and r0+u*R < n <= 64)
+        const int src = ((r0 + u * R) & (kWave - 1)) * 4 + slot4;
+        uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
+        off = live ? off : kNoRow;
+        d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off + col), 0, 0));
+        if constexpr (HDR) h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
+        else h[u] = 0u;
+        if constexpr (WEIGHTED) w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
+        else w[u] = 1.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (r0 + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, d[u], h[u], w[u], p.fp8);
+      }
+    }
+  }
+
+  reduce_slots<E, HDR>(acc, bacc, LG);
+  if (slot == 0 && col_ok) finish_bag<WT>(p, td, L, dw, b, acc, bacc);
+}
+
+// ---------------------------------------------------------------- pooled bag, 64-bit tables
+
+// Same contract for tables whose rows span 2 GiB or more: 64-bit addresses and
+// explicit masks instead of the buffer range check.  Lanes per row are a runtime
+// value here.
+template <int WT, bool WEIGHTED>
+__device__ __forceinline__ void pool_bag_wide(const KParams& p, const TbeTableDesc& td, int64_t start, int L,
+                                              int ct, int64_t b) {
   constexpr int E = Traits<WT>::kEpd;
   constexpr bool HDR = Traits<WT>::kHdr;
   const int lane = threadIdx.x & (kWave - 1);
@@ -263,10 +552,8 @@ __device__ __forceinline__ void pool_bag(const KParams& p, const TbeTableDesc& t
   const bool col_ok = dw < td.data_dwords;
   const uint8_t* tbase = p.weights + td.weights_offset;
   const uint8_t* lane_base = tbase + td.data_offset + 4 * dw;
-  const IndexT* ind = static_cast<const IndexT*>(p.indices) + start;
-  const float* psw = WEIGHTED ? p.psw + start : nullptr;
   const int64_t rows = td.num_rows;
-  const int stride = td.row_stride;
+  const int64_t stride = td.row_stride;
 
   float acc[E];
 #pragma unroll
@@ -275,29 +562,33 @@ __device__ __forceinline__ void pool_bag(const KParams& p, const TbeTableDesc& t
 
   for (int base = 0; base < L; base += kWave) {
     const int n = min(kWave, L - base);
-    // stage up to 64 indices (and weights) of the bag: one coalesced load
-    int my_row = -1;
+    int64_t my_row = -1;
     float my_w = 0.f;
     if (lane < n) {
-      const int64_t idx = static_cast<int64_t>(ind[base + lane]);
-      if (idx >= 0 && idx < rows) my_row = static_cast<int>(idx);
-      if constexpr (WEIGHTED) my_w = psw[base + lane];
+      const int64_t idx = load_index(p, p.indices, start + base + lane);
+      if (idx >= 0 && idx < rows) my_row = idx;
+      if constexpr (WEIGHTED) my_w = p.psw[start + base + lane];
     }
-    for (int r0 = 0; r0 < n; r0 += R * kUnroll) {
-      uint32_t d[kUnroll], h[kUnroll];
-      float w[kUnroll];
+    const int32_t row_lo = static_cast<int32_t>(my_row);
+    const int32_t row_hi = static_cast<int32_t>(my_row >> 32);
+    for (int r0 = 0; r0 < n; r0 += R * kUnrollWide) {
+      uint32_t d[kUnrollWide], h[kUnrollWide];
+      float w[kUnrollWide];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < kUnrollWide; ++u) {
         d[u] = 0u;
         h[u] = 0u;
         w[u] = 0.f;
         if (r0 + u * R < n) {  // wave-uniform
           const int i = r0 + u * R + slot;
-          const int row = __shfl(my_row, i & (kWave - 1));
+          const int src = (i & (kWave - 1)) * 4;
+          const int64_t row = static_cast<int64_t>(
+              (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, row_hi))) << 32) |
+              static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, row_lo)));
           float wi = 1.f;
-          if constexpr (WEIGHTED) wi = __shfl(my_w, i & (kWave - 1));
+          if constexpr (WEIGHTED) wi = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
           if (i < n && row >= 0) {
-            const int64_t roff = static_cast<int64_t>(row) * stride;
+            const int64_t roff = row * stride;
             if (col_ok) d[u] = load_word(lane_base + roff);
             if constexpr (HDR) h[u] = load_word(tbase + roff);
             w[u] = wi;
@@ -305,79 +596,93 @@ __device__ __forceinline__ void pool_bag(const KParams& p, const TbeTableDesc& t
         }
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (r0 + u * R < n) {
-          float v[E];
-          decode<WT>(d[u], v, p.fp8);
-          if constexpr (HDR) {
-            float s = half_bits_to_float(h[u] & 0xFFFFu);
-            float bi = half_bits_to_float(h[u] >> 16);
-            if constexpr (WEIGHTED) {
-              s *= w[u];
-              bi *= w[u];
-            }
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[e] = fmaf(v[e], s, acc[e]);
-            bacc += bi;
-          } else if constexpr (WEIGHTED) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[e] = fmaf(v[e], w[u], acc[e]);
-          } else {
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[e] += v[e];
-          }
-        }
-      }
+      for (int u = 0; u < kUnrollWide; ++u)
+        if (r0 + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, d[u], h[u], w[u], p.fp8);
     }
   }
 
-  // reduce the R row slots (lanes that differ in bits lg..5)
-  for (int off = kWave >> 1; off >= (1 << lg); off >>= 1) {
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] += __shfl_xor(acc[e], off);
-    if constexpr (HDR) bacc += __shfl_xor(bacc, off);
-  }
+  reduce_slots<E, HDR>(acc, bacc, lg);
+  if (slot == 0 && col_ok) finish_bag<WT>(p, td, L, dw, b, acc, bacc);
+}
 
-  if (slot == 0 && col_ok) {
-    const float scale = (p.mean && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;  // P:355
-    float r[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float x = HDR ? acc[e] + bacc : acc[e];
-      r[e] = p.mean ? x * scale : x;
-    }
-    OutT* o = static_cast<OutT*>(p.out) + b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E;
-    store_slice<OutT, E>(o, r);
+// ---------------------------------------------------------------- pooled kernels
+
+// Work item -> bag of the group: table, sample, column tile and the bag's index
+// range.  Returns false when the item's column tile does not exist for its table.
+__device__ __forceinline__ bool item_bag(const KParams& p, uint32_t item, TbeTableDesc& td, int64_t& start,
+                                         int& L, int& ct, int64_t& b) {
+  uint32_t k = item;
+  ct = 0;
+  if (p.col_tiles > 1) {
+    k = fast_div(item, p.div_tiles);
+    ct = static_cast<int>(item - k * static_cast<uint32_t>(p.col_tiles));
+  }
+  const uint32_t gt = static_cast<uint32_t>(uniform(static_cast<int>(fast_div(k, p.div_B))));
+  b = static_cast<int64_t>(k - gt * static_cast<uint32_t>(p.B));
+  const int32_t t = p.order ? load_uniform(p.order + p.group_first + gt) : static_cast<int32_t>(gt);
+  td = load_desc(p.tables + t);
+  if (ct >= td.col_tiles) return false;
+  const int64_t bag = static_cast<int64_t>(t) * p.B + b;
+  // clamp to the index array so malformed offsets can never read out of bounds
+  start = min(max(load_offset(p, bag), int64_t(0)), p.num_indices);
+  const int64_t end = min(max(load_offset(p, bag + 1), start), p.num_indices);
+  L = static_cast<int>(end - start);
+  return true;
+}
+
+// Items [first, end) of this wave, stepping by `step`: one contiguous range per
+// XCD, interleaved over the XCD's waves.
+struct WaveItems {
+  uint32_t first, end, step;
+};
+
+__device__ __forceinline__ WaveItems wave_items(const KParams& p) {
+  const uint32_t wv = static_cast<uint32_t>(uniform(threadIdx.x >> 6));
+  // every partition must own at least one block
+  const uint32_t nparts = p.xcd ? min(static_cast<uint32_t>(kNumXcd), gridDim.x) : 1u;
+  const uint32_t part = blockIdx.x % nparts;
+  const uint32_t lblk = blockIdx.x / nparts;
+  const uint32_t nblk = (gridDim.x - part + nparts - 1) / nparts;  // blocks of this partition
+  const uint32_t I = static_cast<uint32_t>(p.num_items);
+  WaveItems w;
+  w.first = static_cast<uint32_t>(static_cast<uint64_t>(I) * part / nparts) + lblk * kWavesPerBlock + wv;
+  w.end = static_cast<uint32_t>(static_cast<uint64_t>(I) * (part + 1) / nparts);
+  w.step = nblk * kWavesPerBlock;
+  return w;
+}
+
+// Kernel for one group of 32-bit tables with weight type WT and 2^LG lanes per row.
+template <int WT, int LG, bool WEIGHTED>
+__global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
+  const WaveItems w = wave_items(p);
+  for (uint32_t item = w.first; item < w.end; item += w.step) {
+    TbeTableDesc td;
+    int64_t start, b;
+    int L, ct;
+    if (!item_bag(p, item, td, start, L, ct, b)) continue;
+    pool_bag_fast<WT, LG, WEIGHTED>(p, td, start, L, ct, b);
   }
 }
 
-template <typename IndexT, typename OutT, bool WEIGHTED>
-__global__ __launch_bounds__(kBlock) void pooled_kernel(KParams p) {
-  int blk = blockIdx.x;
-  if (p.xcd_remap) blk = remap_block(blk, p.num_blocks);
-  const int wv = uniform(threadIdx.x >> 6);
-  const int64_t item = static_cast<int64_t>(blk) * kWavesPerBlock + wv;
-  if (item >= p.num_items) return;
-  const int64_t k = item / p.col_tiles;
-  const int ct = static_cast<int>(item - k * p.col_tiles);
-  const int t = static_cast<int>(k / p.B);
-  const int64_t b = k - static_cast<int64_t>(t) * p.B;
-  const TbeTableDesc td = p.tables[t];
-  if (ct >= td.col_tiles) return;
-  const IndexT* offs = static_cast<const IndexT*>(p.offsets);
-  // clamp to the index array so malformed offsets can never read out of bounds
-  const int64_t start = min(max(static_cast<int64_t>(offs[k]), int64_t(0)), p.num_indices);
-  const int64_t end = min(max(static_cast<int64_t>(offs[k + 1]), start), p.num_indices);
-  const int L = static_cast<int>(end - start);
-  switch (td.weight_ty) {
-    case TBE_TY_INT4: pool_bag<TBE_TY_INT4, IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    case TBE_TY_INT8: pool_bag<TBE_TY_INT8, IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    case TBE_TY_INT2: pool_bag<TBE_TY_INT2, IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    case TBE_TY_FP8:  pool_bag<TBE_TY_FP8,  IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    case TBE_TY_FP16: pool_bag<TBE_TY_FP16, IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    case TBE_TY_BF16: pool_bag<TBE_TY_BF16, IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    case TBE_TY_FP32: pool_bag<TBE_TY_FP32, IndexT, OutT, WEIGHTED>(p, td, start, L, ct, b); break;
-    default: break;  // rejected by the planner
+// Kernel for a group of 64-bit tables (any weight type, runtime lanes per row).
+template <bool WEIGHTED>
+__global__ __launch_bounds__(kBlock) void pooled_wide_kernel(KParams p) {
+  const WaveItems w = wave_items(p);
+  for (uint32_t item = w.first; item < w.end; item += w.step) {
+    TbeTableDesc td;
+    int64_t start, b;
+    int L, ct;
+    if (!item_bag(p, item, td, start, L, ct, b)) continue;
+    switch (td.weight_ty) {
+      case TBE_TY_INT4: pool_bag_wide<TBE_TY_INT4, WEIGHTED>(p, td, start, L, ct, b); break;
+      case TBE_TY_INT8: pool_bag_wide<TBE_TY_INT8, WEIGHTED>(p, td, start, L, ct, b); break;
+      case TBE_TY_INT2: pool_bag_wide<TBE_TY_INT2, WEIGHTED>(p, td, start, L, ct, b); break;
+      case TBE_TY_FP8:  pool_bag_wide<TBE_TY_FP8,  WEIGHTED>(p, td, start, L, ct, b); break;
+      case TBE_TY_FP16: pool_bag_wide<TBE_TY_FP16, WEIGHTED>(p, td, start, L, ct, b); break;
+      case TBE_TY_BF16: pool_bag_wide<TBE_TY_BF16, WEIGHTED>(p, td, start, L, ct, b); break;
+      case TBE_TY_FP32: pool_bag_wide<TBE_TY_FP32, WEIGHTED>(p, td, start, L, ct, b); break;
+      default: break;  // rejected by the planner
+    }
   }
 }
 
@@ -385,9 +690,8 @@ __global__ __launch_bounds__(kBlock) void pooled_kernel(KParams p) {
 
 // Rows [i0, i1) of the global index array, all belonging to table td: output row i
 // is the dequantized row of indices[i] (N:224-300).
-template <int WT, typename IndexT, typename OutT>
-__device__ __forceinline__ void nobag_rows(const KParams& p, const TbeTableDesc& td, int64_t i0,
-                                           int64_t i1) {
+template <int WT>
+__device__ __forceinline__ void nobag_rows(const KParams& p, const TbeTableDesc& td, int64_t i0, int64_t i1) {
   constexpr int E = Traits<WT>::kEpd;
   constexpr bool HDR = Traits<WT>::kHdr;
   const int lane = threadIdx.x & (kWave - 1);
@@ -395,14 +699,13 @@ __device__ __forceinline__ void nobag_rows(const KParams& p, const TbeTableDesc&
   const int R = kWave >> lg;
   const int slot = lane >> lg;
   const uint8_t* tbase = p.weights + td.weights_offset;
-  const IndexT* ind = static_cast<const IndexT*>(p.indices);
   for (int ct = 0; ct < td.col_tiles; ++ct) {
     const int dw = ct * kWave + (lane & ((1 << lg) - 1));
     const bool col_ok = dw < td.data_dwords;
     for (int64_t r0 = i0; r0 < i1; r0 += R) {
       const int64_t i = r0 + slot;
       if (i >= i1 || !col_ok) continue;
-      const int64_t idx = static_cast<int64_t>(ind[i]);
+      const int64_t idx = load_index(p, p.indices, i);
       float v[E];
       float s = 1.f, bi = 0.f;
       if (idx >= 0 && idx < td.num_rows) {
@@ -410,8 +713,8 @@ __device__ __forceinline__ void nobag_rows(const KParams& p, const TbeTableDesc&
         decode<WT>(load_word(row + td.data_offset + 4 * dw), v, p.fp8);
         if constexpr (HDR) {
           const uint32_t h = load_word(row);
-          s = half_bits_to_float(h & 0xFFFFu);
-          bi = half_bits_to_float(h >> 16);
+          s = h16lo(h);
+          bi = h16hi(h);
         }
       } else {
 #pragma unroll
@@ -420,19 +723,12 @@ __device__ __forceinline__ void nobag_rows(const KParams& p, const TbeTableDesc&
       }
       float r[E];
 #pragma unroll
-      for (int e = 0; e < E; ++e) r[e] = HDR ? fmaf(v[e], s, bi) : v[e];
-      OutT* o = static_cast<OutT*>(p.out) + i * p.out_stride + static_cast<int64_t>(dw) * E;
-      store_slice<OutT, E>(o, r);
+      for (int e = 0; e < E; ++e) r[e] = HDR ? fmaf(s, v[e], bi) : v[e];
+      store_out<E>(p, i * p.out_stride + static_cast<int64_t>(dw) * E, r);
     }
   }
 }
 
-template <typename IndexT>
-__device__ __forceinline__ int64_t table_begin(const KParams& p, int t) {
-  return static_cast<int64_t>(static_cast<const IndexT*>(p.offsets)[static_cast<int64_t>(t) * p.B]);
-}
-
-template <typename IndexT, typename OutT>
 __global__ __launch_bounds__(kBlock) void nobag_kernel(KParams p) {
   const int wv = uniform(threadIdx.x >> 6);
   const int64_t item = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wv;
@@ -443,23 +739,23 @@ __global__ __launch_bounds__(kBlock) void nobag_kernel(KParams p) {
   int lo = 0, hi = p.T - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (table_begin<IndexT>(p, mid) <= i0) lo = mid; else hi = mid - 1;
+    if (load_offset(p, static_cast<int64_t>(mid) * p.B) <= i0) lo = mid; else hi = mid - 1;
   }
   for (int t = lo; t < p.T; ++t) {
-    const int64_t tb = table_begin<IndexT>(p, t);
-    const int64_t te = table_begin<IndexT>(p, t + 1);
+    const int64_t tb = load_offset(p, static_cast<int64_t>(t) * p.B);
+    const int64_t te = load_offset(p, static_cast<int64_t>(t + 1) * p.B);
     if (tb >= i1) break;
     const int64_t a = max(tb, i0), e = min(te, i1);
     if (a >= e) continue;
-    const TbeTableDesc td = p.tables[t];
+    const TbeTableDesc td = load_desc(p.tables + t);
     switch (td.weight_ty) {
-      case TBE_TY_INT4: nobag_rows<TBE_TY_INT4, IndexT, OutT>(p, td, a, e); break;
-      case TBE_TY_INT8: nobag_rows<TBE_TY_INT8, IndexT, OutT>(p, td, a, e); break;
-      case TBE_TY_INT2: nobag_rows<TBE_TY_INT2, IndexT, OutT>(p, td, a, e); break;
-      case TBE_TY_FP8:  nobag_rows<TBE_TY_FP8,  IndexT, OutT>(p, td, a, e); break;
-      case TBE_TY_FP16: nobag_rows<TBE_TY_FP16, IndexT, OutT>(p, td, a, e); break;
-      case TBE_TY_BF16: nobag_rows<TBE_TY_BF16, IndexT, OutT>(p, td, a, e); break;
-      case TBE_TY_FP32: nobag_rows<TBE_TY_FP32, IndexT, OutT>(p, td, a, e); break;
+      case TBE_TY_INT4: nobag_rows<TBE_TY_INT4>(p, td, a, e); break;
+      case TBE_TY_INT8: nobag_rows<TBE_TY_INT8>(p, td, a, e); break;
+      case TBE_TY_INT2: nobag_rows<TBE_TY_INT2>(p, td, a, e); break;
+      case TBE_TY_FP8:  nobag_rows<TBE_TY_FP8>(p, td, a, e); break;
+      case TBE_TY_FP16: nobag_rows<TBE_TY_FP16>(p, td, a, e); break;
+      case TBE_TY_BF16: nobag_rows<TBE_TY_BF16>(p, td, a, e); break;
+      case TBE_TY_FP32: nobag_rows<TBE_TY_FP32>(p, td, a, e); break;
       default: break;
     }
   }
@@ -499,41 +795,84 @@ Fp8Consts make_fp8(int bits, int bias) {
   const uint32_t mult_bits = static_cast<uint32_t>(254 - bias) << 23;
   memcpy(&c.mult, &mult_bits, 4);
   c.sub_scale = ldexpf(1.0f, 1 - bias - (7 - bits));
+  c.h16_shift = static_cast<uint32_t>(bits + 3);
+  c.h16_scale = ldexpf(1.0f, 15 - bias);
+  c.h16_ok = bits <= 4;
   return c;
 }
 
-template <typename IndexT, typename OutT>
-hipError_t launch_pooled(const KParams& p, bool weighted, hipStream_t s) {
-  if (weighted)
-    hipLaunchKernelGGL((pooled_kernel<IndexT, OutT, true>), dim3(p.num_blocks), dim3(kBlock), 0, s, p);
-  else
-    hipLaunchKernelGGL((pooled_kernel<IndexT, OutT, false>), dim3(p.num_blocks), dim3(kBlock), 0, s, p);
-  return hipGetLastError();
+FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{};
+  f.d = d;
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  f.shift = l;
+  f.mul = static_cast<uint32_t>(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+  return f;
 }
 
-template <typename IndexT>
-hipError_t launch_pooled_out(const KParams& p, int out_ty, bool weighted, hipStream_t s) {
-  switch (out_ty) {
-    case TBE_TY_FP32: return launch_pooled<IndexT, float>(p, weighted, s);
-    case TBE_TY_FP16: return launch_pooled<IndexT, _Float16>(p, weighted, s);
-    default: return launch_pooled<IndexT, Bf16Out>(p, weighted, s);
+using KernelFn = void (*)(KParams);
+
+template <int WT, int LG>
+KernelFn fast_kernel_for(bool weighted) {
+  return weighted ? pooled_fast_kernel<WT, LG, true> : pooled_fast_kernel<WT, LG, false>;
+}
+
+template <int WT>
+KernelFn fast_kernel_lg(int lg, bool weighted) {
+  switch (lg) {
+    case 0: return fast_kernel_for<WT, 0>(weighted);
+    case 1: return fast_kernel_for<WT, 1>(weighted);
+    case 2: return fast_kernel_for<WT, 2>(weighted);
+    case 3: return fast_kernel_for<WT, 3>(weighted);
+    case 4: return fast_kernel_for<WT, 4>(weighted);
+    case 5: return fast_kernel_for<WT, 5>(weighted);
+    default: return fast_kernel_for<WT, 6>(weighted);
   }
 }
 
-template <typename IndexT>
-hipError_t launch_nobag_out(const KParams& p, int out_ty, hipStream_t s) {
-  switch (out_ty) {
-    case TBE_TY_FP32:
-      hipLaunchKernelGGL((nobag_kernel<IndexT, float>), dim3(p.num_blocks), dim3(kBlock), 0, s, p);
-      break;
-    case TBE_TY_FP16:
-      hipLaunchKernelGGL((nobag_kernel<IndexT, _Float16>), dim3(p.num_blocks), dim3(kBlock), 0, s, p);
-      break;
-    default:
-      hipLaunchKernelGGL((nobag_kernel<IndexT, Bf16Out>), dim3(p.num_blocks), dim3(kBlock), 0, s, p);
-      break;
+KernelFn pooled_kernel_for(const TbePlanGroup& g, bool weighted) {
+  if (!g.offset32) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
+  switch (g.weight_ty) {
+    case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, weighted);
+    case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, weighted);
+    case TBE_TY_BF16: return fast_kernel_lg<TBE_TY_BF16>(g.log2_lanes, weighted);
+    case TBE_TY_FP8:  return fast_kernel_lg<TBE_TY_FP8>(g.log2_lanes, weighted);
+    case TBE_TY_INT8: return fast_kernel_lg<TBE_TY_INT8>(g.log2_lanes, weighted);
+    case TBE_TY_INT4: return fast_kernel_lg<TBE_TY_INT4>(g.log2_lanes, weighted);
+    default:          return fast_kernel_lg<TBE_TY_INT2>(g.log2_lanes, weighted);
   }
-  return hipGetLastError();
+}
+
+// Blocks of `fn` the whole GPU keeps resident at once (cached per device and kernel).
+int resident_blocks(KernelFn fn) {
+  static std::mutex mu;
+  static std::vector<std::pair<std::pair<int, KernelFn>, int>> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> g(mu);
+  for (auto& e : cache)
+    if (e.first.first == dev && e.first.second == fn) return e.second;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), kBlock, 0) !=
+      hipSuccess)
+    return 0;
+  const int blocks = std::max(1, cus * per_cu);
+  cache.push_back({{dev, fn}, blocks});
+  return blocks;
+}
+
+hipError_t launch(KernelFn fn, KParams& p, int64_t want_blocks, bool persistent, hipStream_t s) {
+  int64_t blocks = want_blocks;
+  if (persistent) {
+    const int cap = resident_blocks(fn);
+    if (cap > 0) blocks = std::min<int64_t>(blocks, cap);
+  }
+  blocks = std::max<int64_t>(1, blocks);
+  void* args[] = {&p};
+  return hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3(static_cast<uint32_t>(blocks)), dim3(kBlock),
+                         args, 0, s);
 }
 
 }  // namespace tbe
@@ -546,9 +885,9 @@ const char* tbe_last_error(void) { return g_last_error.c_str(); }
 
 int tbe_nbit_abi_version(void) { return TBE_NBIT_ABI_VERSION; }
 
-int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, TbePlanSummary* summary) {
+int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_order, TbePlanSummary* summary) {
   g_last_error.clear();
-  if (!in || !descs || !summary) return fail(TBE_ERR_INVALID_ARG, "null argument to tbe_nbit_plan");
+  if (!in || !descs || !table_order || !summary) return fail(TBE_ERR_INVALID_ARG, "null argument to tbe_nbit_plan");
   const int T = in->T;
   // A:116, H:120-123
   if (T <= 0) return fail(TBE_ERR_INVALID_ARG, "weights_offsets size must be greater than 0 (got T=%d)", T);
@@ -612,6 +951,7 @@ int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, TbePlanSummary* s
     auto it = std::upper_bound(starts.begin(), starts.end(), descs[t].weights_offset);
     const int64_t end = it == starts.end() ? in->dev_weights_bytes : *it;
     descs[t].num_rows = (end - descs[t].weights_offset) / descs[t].row_stride;
+    if (descs[t].num_rows * descs[t].row_stride <= 0x7FFFFFFFLL) descs[t].flags |= TBE_TABLE_OFFSET32;
   }
   if (has_fp8) {
     const int eb = in->fp8_exponent_bits, bias = in->fp8_exponent_bias;
@@ -620,6 +960,36 @@ int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, TbePlanSummary* s
                   eb, bias);
   }
   s.has_fp8 = has_fp8;
+  // group tables by kernel specialisation; table order is kept inside a group so
+  // that the XCD split of a group's bags still follows table boundaries
+  auto key = [&](int t) {
+    const TbeTableDesc& d = descs[t];
+    const bool o32 = d.flags & TBE_TABLE_OFFSET32;
+    return o32 ? (d.weight_ty * 8 + d.log2_lanes) : 1000;  // 64-bit tables share one generic kernel
+  };
+  std::vector<int32_t> order(T);
+  for (int t = 0; t < T; ++t) order[t] = t;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) < key(b); });
+  s.num_groups = 0;
+  for (int i = 0; i < T;) {
+    int j = i;
+    int tiles = 1;
+    while (j < T && key(order[j]) == key(order[i])) {
+      tiles = std::max<int>(tiles, descs[order[j]].col_tiles);
+      ++j;
+    }
+    if (s.num_groups >= TBE_MAX_GROUPS) return fail(TBE_ERR_UNSUPPORTED, "too many table groups");
+    TbePlanGroup& g = s.groups[s.num_groups++];
+    const TbeTableDesc& d0 = descs[order[i]];
+    g.offset32 = (d0.flags & TBE_TABLE_OFFSET32) ? 1 : 0;
+    g.weight_ty = g.offset32 ? d0.weight_ty : -1;
+    g.log2_lanes = g.offset32 ? d0.log2_lanes : -1;
+    g.first = i;
+    g.count = j - i;
+    g.col_tiles = tiles;
+    i = j;
+  }
+  memcpy(table_order, order.data(), sizeof(int32_t) * T);
   *summary = s;
   return TBE_OK;
 }
@@ -641,47 +1011,62 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
                 a->output_dtype);
   if (a->max_col_tiles < 1 || a->max_col_tiles > 255) return fail(TBE_ERR_INVALID_ARG, "bad max_col_tiles");
   if (a->num_indices < 0) return fail(TBE_ERR_INVALID_ARG, "negative num_indices");
+  if (static_cast<int64_t>(a->T) * a->B * a->max_col_tiles > 0x7FFFFFFF)
+    return fail(TBE_ERR_UNSUPPORTED, "too many bags for one call (T*B*col_tiles >= 2^31)");
+  const int64_t nbags = static_cast<int64_t>(a->T) * a->B;
+  if (a->pooling_mode == TBE_POOL_NONE ? a->num_indices == 0 : nbags == 0) return TBE_OK;
+  if (!a->dev_weights || !a->tables || !a->offsets || !a->output || !a->plan)
+    return fail(TBE_ERR_INVALID_ARG, "null pointer argument");
+  if (a->num_indices > 0 && !a->indices) return fail(TBE_ERR_INVALID_ARG, "null indices");
+
   KParams p{};
   p.weights = a->dev_weights;
   p.tables = a->tables;
+  p.order = a->table_order;
   p.indices = a->indices;
   p.offsets = a->offsets;
   p.psw = a->indice_weights;
   p.out = a->output;
   p.out_stride = a->output_stride;
-  p.B = a->B;
   p.num_indices = a->num_indices;
+  p.B = static_cast<int32_t>(a->B);
   p.T = a->T;
-  p.col_tiles = a->max_col_tiles;
-  p.xcd_remap = (a->flags & TBE_FLAG_NO_XCD_REMAP) ? 0 : 1;
+  p.index64 = a->index_size == 8;
+  p.out_ty = a->output_dtype;
   p.mean = a->pooling_mode == TBE_POOL_MEAN;
+  p.xcd = (a->flags & TBE_FLAG_NO_XCD_REMAP) ? 0 : 1;
   p.fp8 = make_fp8(a->fp8_exponent_bits, a->fp8_exponent_bias);
+  p.div_B = make_fastdiv(static_cast<uint32_t>(std::max<int64_t>(a->B, 1)));
   hipStream_t s = static_cast<hipStream_t>(hip_stream);
-  hipError_t err;
+
   if (a->pooling_mode == TBE_POOL_NONE) {
-    p.num_items = (a->num_indices + kWave - 1) / kWave;
-    if (p.num_items == 0) return TBE_OK;
-    const int64_t blocks = (p.num_items + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (blocks > 0x7FFFFFFF) return fail(TBE_ERR_UNSUPPORTED, "too many indices for one launch");
-    if (!a->dev_weights || !a->tables || !a->indices || !a->offsets || !a->output)
-      return fail(TBE_ERR_INVALID_ARG, "null device pointer");
-    p.num_blocks = static_cast<int32_t>(blocks);
-    err = a->index_size == 8 ? launch_nobag_out<int64_t>(p, a->output_dtype, s)
-                             : launch_nobag_out<int32_t>(p, a->output_dtype, s);
-  } else {
-    p.num_items = static_cast<int64_t>(a->T) * a->B * a->max_col_tiles;
-    if (p.num_items == 0) return TBE_OK;
-    const int64_t blocks = (p.num_items + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (blocks > 0x7FFFFFFF) return fail(TBE_ERR_UNSUPPORTED, "too many bags for one launch");
-    if (!a->dev_weights || !a->tables || !a->offsets || !a->output)
-      return fail(TBE_ERR_INVALID_ARG, "null device pointer");
-    if (a->num_indices > 0 && !a->indices) return fail(TBE_ERR_INVALID_ARG, "null indices");
-    p.num_blocks = static_cast<int32_t>(blocks);
-    const bool weighted = a->indice_weights != nullptr;
-    err = a->index_size == 8 ? launch_pooled_out<int64_t>(p, a->output_dtype, weighted, s)
-                             : launch_pooled_out<int32_t>(p, a->output_dtype, weighted, s);
+    const int64_t chunks = (a->num_indices + kWave - 1) / kWave;
+    if (chunks > 0x7FFFFFFF) return fail(TBE_ERR_UNSUPPORTED, "too many indices for one launch");
+    p.num_items = static_cast<int32_t>(chunks);
+    p.order = nullptr;
+    const hipError_t err = launch(nobag_kernel, p, (chunks + kWavesPerBlock - 1) / kWavesPerBlock, false, s);
+    if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    return TBE_OK;
   }
-  if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+
+  if (!a->table_order) return fail(TBE_ERR_INVALID_ARG, "null table_order");
+  const TbePlanSummary& plan = *a->plan;
+  if (plan.num_groups < 1 || plan.num_groups > TBE_MAX_GROUPS) return fail(TBE_ERR_INVALID_ARG, "bad plan");
+  const bool weighted = a->indice_weights != nullptr;
+  for (int gi = 0; gi < plan.num_groups; ++gi) {
+    const TbePlanGroup& g = plan.groups[gi];
+    if (g.count <= 0 || g.first < 0 || g.first + g.count > a->T || g.col_tiles < 1 || g.col_tiles > 255)
+      return fail(TBE_ERR_INVALID_ARG, "bad plan group %d", gi);
+    p.group_first = g.first;
+    p.group_count = g.count;
+    p.col_tiles = g.col_tiles;
+    p.div_tiles = make_fastdiv(static_cast<uint32_t>(g.col_tiles));
+    const int64_t items = static_cast<int64_t>(g.count) * a->B * g.col_tiles;
+    p.num_items = static_cast<int32_t>(items);
+    const hipError_t err = launch(pooled_kernel_for(g, weighted), p,
+                                  (items + kWavesPerBlock - 1) / kWavesPerBlock, true, s);
+    if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  }
   return TBE_OK;
 }
 

@@ -19,6 +19,7 @@
 #include <torch/library.h>
 
 #include <list>
+#include <memory>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -57,8 +58,13 @@ struct PlanKey {
 };
 
 struct Plan {
-  Tensor device_descs;  // uint8 [T * sizeof(TbeTableDesc)] on the weights' device
-  TbePlanSummary summary;
+  // one device buffer: TbeTableDesc[T] followed by the int32 table order [T]
+  Tensor device_plan;
+  std::shared_ptr<TbePlanSummary> summary;  // host copy, handed to every forward
+  const TbeTableDesc* descs() const { return reinterpret_cast<const TbeTableDesc*>(device_plan.data_ptr<uint8_t>()); }
+  const int32_t* order(int64_t T) const {
+    return reinterpret_cast<const int32_t*>(device_plan.data_ptr<uint8_t>() + T * sizeof(TbeTableDesc));
+  }
 };
 
 class PlanCache {
@@ -97,13 +103,16 @@ class PlanCache {
     in.fp8_exponent_bits = static_cast<int32_t>(key.fp8_bits);
     in.fp8_exponent_bias = static_cast<int32_t>(key.fp8_bias);
     std::vector<TbeTableDesc> descs(key.T);
+    std::vector<int32_t> order(key.T);
     Plan p{};
-    const int rc = tbe_nbit_plan(&in, descs.data(), &p.summary);
+    p.summary = std::make_shared<TbePlanSummary>();
+    const int rc = tbe_nbit_plan(&in, descs.data(), order.data(), p.summary.get());
     TORCH_CHECK(rc == TBE_OK, "int_nbit_split_embedding_codegen_lookup_function: ", tbe_last_error());
-    Tensor host = at::empty({static_cast<int64_t>(descs.size() * sizeof(TbeTableDesc))},
-                            at::TensorOptions().dtype(at::kByte));
-    memcpy(host.data_ptr<uint8_t>(), descs.data(), descs.size() * sizeof(TbeTableDesc));
-    p.device_descs = host.to(dev);
+    const size_t dbytes = descs.size() * sizeof(TbeTableDesc), obytes = order.size() * sizeof(int32_t);
+    Tensor host = at::empty({static_cast<int64_t>(dbytes + obytes)}, at::TensorOptions().dtype(at::kByte));
+    memcpy(host.data_ptr<uint8_t>(), descs.data(), dbytes);
+    memcpy(host.data_ptr<uint8_t>() + dbytes, order.data(), obytes);
+    p.device_plan = host.to(dev);
     return p;
   }
 
@@ -179,11 +188,13 @@ Tensor int_nbit_split_embedding_codegen_lookup_function_hip(
                     T, dev_weights.numel(), row_align, fp8_bits, fp8_bias,
                     static_cast<int>(dev_weights.get_device())};
   const Plan plan = plan_cache().get(key, weights_offsets, weights_tys, D_offsets, dev_weights.device());
-  const TbePlanSummary& s = plan.summary;
+  const TbePlanSummary& s = *plan.summary;
 
   TbeNbitArgs a{};
   a.dev_weights = dev_weights.data_ptr<uint8_t>();
-  a.tables = reinterpret_cast<const TbeTableDesc*>(plan.device_descs.data_ptr<uint8_t>());
+  a.tables = plan.descs();
+  a.table_order = plan.order(T);
+  a.plan = plan.summary.get();
   a.T = static_cast<int32_t>(T);
   a.max_col_tiles = s.max_col_tiles;
   a.indices = idx.data_ptr();

@@ -69,8 +69,12 @@ typedef struct TbeTableDesc {
   uint8_t weight_ty;      /* TbeSparseType                                        */
   uint8_t log2_lanes;     /* lanes of a 64-wide wavefront that share one row     */
   uint8_t col_tiles;      /* 256-byte column tiles per row (>1 only for wide rows)*/
-  uint8_t reserved;
+  uint8_t flags;          /* TBE_TABLE_* bits, set by the planner                 */
 } TbeTableDesc;
+
+/* TbeTableDesc.flags: the table's rows span < 2 GiB, so the kernels address them
+ * with 32-bit offsets from the table base (buffer loads with range checking). */
+#define TBE_TABLE_OFFSET32 0x1
 
 /* Host-side table metadata handed to the planner (all host pointers). */
 typedef struct TbePlanInput {
@@ -84,6 +88,21 @@ typedef struct TbePlanInput {
   int32_t fp8_exponent_bias;       /* -1 when no FP8 table                      */
 } TbePlanInput;
 
+/*
+ * Tables that share one kernel specialisation: same weight type, same lanes per
+ * row, same addressing mode.  Their ids are table_order[first .. first+count).
+ */
+typedef struct TbePlanGroup {
+  int32_t weight_ty;      /* TbeSparseType                                         */
+  int32_t log2_lanes;     /* as in TbeTableDesc                                    */
+  int32_t offset32;       /* 1: all rows addressed with 32-bit offsets             */
+  int32_t first;          /* position in table_order                               */
+  int32_t count;          /* tables in the group                                   */
+  int32_t col_tiles;      /* max col_tiles over the group's tables                 */
+} TbePlanGroup;
+
+#define TBE_MAX_GROUPS 64
+
 /* Summary of a plan: what the launcher needs beyond the per-table array. */
 typedef struct TbePlanSummary {
   int32_t max_col_tiles;  /* max over tables of col_tiles                          */
@@ -92,6 +111,8 @@ typedef struct TbePlanSummary {
   int32_t uniform_D;      /* 1 if every table has the same D (nobag requirement)   */
   int32_t covers_output;  /* 1 if D_offsets[0]==0 and tables tile [0,total_D)     */
   int32_t has_fp8;        /* 1 if any table is FP8                                 */
+  int32_t num_groups;     /* entries of groups[]                                   */
+  TbePlanGroup groups[TBE_MAX_GROUPS];
 } TbePlanSummary;
 
 /*
@@ -107,6 +128,8 @@ typedef struct TbePlanSummary {
 typedef struct TbeNbitArgs {
   const uint8_t* dev_weights;      /* packed rows of all tables                 */
   const TbeTableDesc* tables;      /* device [T]                                */
+  const int32_t* table_order;      /* device [T], from tbe_nbit_plan            */
+  const TbePlanSummary* plan;      /* HOST pointer, from tbe_nbit_plan          */
   int32_t T;
   int32_t max_col_tiles;           /* from TbePlanSummary                       */
   int64_t B;                       /* bags per table = (len(offsets)-1)/T       */
@@ -128,11 +151,13 @@ typedef struct TbeNbitArgs {
 #define TBE_FLAG_NO_XCD_REMAP 0x1  /* keep the hardware's round-robin block order */
 
 /*
- * Validate the table metadata and fill descs[T] (host memory) and *summary.
- * Mirrors the shape checks of H:95-204 and A:116-151.  Returns TBE_OK or a
- * negative TbeStatus; tbe_last_error() then names the failed check.
+ * Validate the table metadata and fill descs[T], table_order[T] (host memory)
+ * and *summary (which lists the table groups the forward launches one kernel
+ * for).  Mirrors the shape checks of H:95-204 and A:116-151.  Returns TBE_OK or
+ * a negative TbeStatus; tbe_last_error() then names the failed check.
  */
-int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, TbePlanSummary* summary);
+int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_order,
+                  TbePlanSummary* summary);
 
 /*
  * Enqueue the forward on `hip_stream` (a hipStream_t; NULL = default stream).
@@ -146,7 +171,7 @@ const char* tbe_last_error(void);
 
 /* ABI version of this header; bumped on any layout change of the structs above. */
 int tbe_nbit_abi_version(void);
-#define TBE_NBIT_ABI_VERSION 1
+#define TBE_NBIT_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

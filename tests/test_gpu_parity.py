@@ -73,7 +73,11 @@ def _module_from_arrays(pkg, gpu, w, wo, wt, do, pm, out_ty, fp8=(4, 7)):
 def test_kat_bit_exact(pkg, oracle, gpu, idx_dtype, pm):
     rs = np.random.RandomState(7)
     tables = [(37, 16, INT8), (53, 32, INT4), (29, 64, INT2), (41, 8, FP16), (23, 12, FP32),
-              (31, 20, FP8), (19, 6, BF16), (300, 128, INT4), (200, 128, INT8), (50, 4096, FP8)]
+              (31, 20, FP8), (19, 6, BF16), (300, 128, INT4), (200, 128, INT8), (50, 4096, FP8),
+              # every lanes-per-row width (1..64) with and without the scale/bias header
+              (29, 32, INT8), (31, 64, INT4), (33, 128, INT2), (20, 4, FP32), (21, 16, INT2),
+              (22, 8, INT4), (23, 4, INT8), (24, 2, FP16), (25, 32, INT2), (26, 256, INT8),
+              (27, 512, INT4), (28, 64, FP32)]
     B = 13
     w, wo, wt, do, idx, off, vals, lengths = _kat_problem(rs, tables, B, idx_dtype, Lmax=150)
     m = _module_from_arrays(pkg, gpu, w, wo, wt, do, pm, FP32)
@@ -101,6 +105,18 @@ def test_kat_nobag_bit_exact(pkg, oracle, gpu):
 
 
 # ----------------------------------------------------------------- golden library vectors
+
+@pytest.mark.parametrize("B", [1, 2, 7, 31])
+def test_small_batches_cover_every_bag(pkg, oracle, gpu, B):
+    """Launches with fewer blocks than XCDs still pool every bag."""
+    rs = np.random.RandomState(B)
+    tables = [(40, 16, INT8), (30, 32, INT8), (20, 128, INT4)]
+    w, wo, wt, do, idx, off, vals, lengths = _kat_problem(rs, tables, B, np.int64, Lmax=9)
+    m = _module_from_arrays(pkg, gpu, w, wo, wt, do, 0, FP32)
+    out = m(torch.from_numpy(idx).to(gpu), torch.from_numpy(off).to(gpu), None)
+    np.testing.assert_array_equal(out.cpu().numpy(),
+                                  kat_expected(vals, do, idx, off, B, lengths, 0).astype(np.float32))
+
 
 def test_golden_library_vectors_gpu(pkg, golden, gpu):
     for name in [str(n) for n in golden["case_names"]]:

@@ -32,8 +32,8 @@ def test_abi_version_and_struct_layout(pkg, tmp_path):
     """The ctypes mirror has the C compiler's sizes and field offsets for every struct."""
     import subprocess
     c = pkg.capi
-    assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 1
-    structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanSummary, c.TbeNbitArgs]
+    assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 2
+    structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanGroup, c.TbePlanSummary, c.TbeNbitArgs]
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tbe_nbit.h"', "int main(void){"]
     for st in structs:
         lines.append(f'printf("%zu\\n", sizeof({st.__name__}));')
@@ -76,7 +76,7 @@ def test_forward_rejects_bad_args_without_gpu(pkg):
     (FP32, 128, 512, 64, 2), (FP8, 128, 128, 32, 1), (BF16, 64, 128, 32, 1), (INT4, 32, 32, 4, 1),
     (FP8, 4096, 4096, 64, 16), (INT2, 16, 16, 1, 1), (FP8, 12, 16, 4, 1)])
 def test_plan_layout(pkg, ty, D, stride, lanes, tiles):
-    descs, s = pkg.capi.plan([0], [ty], [0, D], 1000 * stride, 16, 4, 7)
+    descs, order, s = pkg.capi.plan([0], [ty], [0, D], 1000 * stride, 16, 4, 7)
     d = descs[0]
     assert (d.row_stride, 1 << d.log2_lanes, d.col_tiles, d.D) == (stride, lanes, tiles, D)
     assert d.data_offset == (4 if ty in (INT8, INT4, INT2) else 0)
@@ -86,9 +86,24 @@ def test_plan_layout(pkg, ty, D, stride, lanes, tiles):
 
 def test_plan_num_rows_follow_table_extents(pkg):
     # tables laid out out of order; rows end where the next table starts
-    descs, s = pkg.capi.plan([800, 0, 400], [INT4, INT8, INT4], [0, 128, 256, 384], 1600)
+    descs, order, s = pkg.capi.plan([800, 0, 400], [INT4, INT8, INT4], [0, 128, 256, 384], 1600)
     assert [descs[i].num_rows for i in range(3)] == [10, 400 // 144, 5]
     assert s.uniform_D == 1 and s.max_D == 128
+
+
+def test_plan_groups_tables_by_kernel_shape(pkg):
+    """Tables are grouped by (weight type, lanes per row), keeping table order in a group."""
+    tys = [INT4, INT8, INT4, FP16, INT4, INT8]
+    Ds = [128, 128, 64, 128, 128, 128]
+    dofs = np.concatenate([[0], np.cumsum(Ds)])
+    woffs = np.arange(6) * 100000
+    descs, order, s = pkg.capi.plan(woffs, tys, dofs, 600000)
+    groups = [(g.weight_ty, g.log2_lanes, g.offset32, g.first, g.count) for g in s.groups[:s.num_groups]]
+    assert sum(g[4] for g in groups) == 6 and len(groups) == 4
+    members = {(g[0], g[1]): list(order[g[3]:g[3] + g[4]]) for g in groups}
+    assert members[(INT4, 4)] == [0, 4] and members[(INT8, 5)] == [1, 5]
+    assert members[(INT4, 3)] == [2] and members[(FP16, 6)] == [3]
+    assert sorted(order.tolist()) == list(range(6))
 
 
 @pytest.mark.parametrize("kw,match", [
