@@ -460,78 +460,249 @@ __device__ __forceinline__ void finish_bag(const KParams& p, const TbeTableDesc&
   store_out<E>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E, r);
 }
 
+// ---------------------------------------------------------------- work items
+
+// Work item -> bag of the group: table, sample, column tile and the bag's index
+// range.  Returns false when the item's column tile does not exist for its table.
+template <typename IndexT>
+__device__ __forceinline__ bool item_bag(const KParams& p, uint32_t item, TbeTableDesc& td, int64_t& start,
+                                         int& L, int& ct, int64_t& b, int32_t& t) {
+  uint32_t k = item;
+  ct = 0;
+  if (p.col_tiles > 1) {
+    k = fast_div(item, p.div_tiles);
+    ct = static_cast<int>(item - k * static_cast<uint32_t>(p.col_tiles));
+  }
+  const uint32_t gt = static_cast<uint32_t>(uniform(static_cast<int>(fast_div(k, p.div_B))));
+  b = static_cast<int64_t>(k - gt * static_cast<uint32_t>(p.B));
+  t = p.order ? load_uniform(p.order + p.group_first + gt) : static_cast<int32_t>(gt);
+  td = load_desc(p.tables + t);
+  if (ct >= td.col_tiles) return false;
+  const int64_t bag = static_cast<int64_t>(t) * p.B + b;
+  // clamp to the index array so malformed offsets can never read out of bounds
+  const IndexT* offs = static_cast<const IndexT*>(p.offsets);
+  start = min(max(static_cast<int64_t>(load_uniform(offs + bag)), int64_t(0)), p.num_indices);
+  const int64_t end = min(max(static_cast<int64_t>(load_uniform(offs + bag + 1)), start), p.num_indices);
+  L = static_cast<int>(end - start);
+  return true;
+}
+
 // ---------------------------------------------------------------- pooled bag, 32-bit tables
 
 // Steps (of R = 64 >> LG rows each) whose loads are issued back to back before
 // any is consumed: 16-32 rows in flight per wave for wide rows, a whole 64-index
-// chunk for short rows.
+// chunk for short rows.  U*R always divides 64, so slot r0 + u*R + slot of a
+// step never passes lane 63 and slots past the bag read lanes holding kNoRow.
 template <int LG>
 constexpr int unroll_for() {
   return LG >= 5 ? 16 : (LG == 4 ? 8 : kWave / (kWave >> LG));
 }
 
-// One wavefront pools bag [start, start+L) of table `td` over column tile `ct`
-// (P:44-85 bag walk, P:282-315 pooling, P:346-394 chunked bag, P:319-342 store)
-// for a table whose rows span < 2 GiB.
-template <int WT, int LG, bool WEIGHTED>
-__device__ __forceinline__ void pool_bag_fast(const KParams& p, const TbeTableDesc& td, int64_t start, int L,
-                                              int ct, int64_t b) {
+// A bag whose first index chunk has been requested: the kernels issue the index
+// load of the next bag before pooling the current one, so that load's latency
+// hides behind the current bag's row loads.  Index chunks are read with buffer
+// loads over exactly the chunk's bytes, so lanes past the chunk get zero from
+// the range check: every path issues the same loads, which keeps the wait
+// counts exact across the software pipeline.
+struct StagedBag {
+  int64_t start;
+  int64_t b;
+  int L;
+  int ct;
+  int32_t t;
+  int valid;
+  uint64_t idx;  // this lane's raw index of chunk 0 (meaningful for lane < min(L, 64))
+  float w;       // its per-sample weight
+};
+
+template <typename IndexT>
+__device__ __forceinline__ uint64_t load_index_chunk(const KParams& p, int64_t first, int n) {
+  // n >= 0 indices from position `first`; lane >= n reads zero
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<IndexT*>(static_cast<const IndexT*>(p.indices) + first), 0,
+      n * static_cast<int>(sizeof(IndexT)), kRsrcWord3);
+  const int lane = threadIdx.x & (kWave - 1);
+  if constexpr (sizeof(IndexT) == 8) {
+    const int lo = __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 8, 0, 0);
+    const int hi = __builtin_amdgcn_raw_buffer_load_b32(rs, lane * 8 + 4, 0, 0);
+    return static_cast<uint64_t>(static_cast<uint32_t>(lo)) | (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32);
+  } else {
+    // sign-extended so a negative int32 index is rejected like a negative int64
+    return static_cast<uint64_t>(static_cast<int64_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, 0, 0)));
+  }
+}
+
+__device__ __forceinline__ float load_weight_chunk(const KParams& p, int64_t first, int n) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.psw + first), 0, n * 4, kRsrcWord3);
+  return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (threadIdx.x & (kWave - 1)) * 4, 0, 0));
+}
+
+template <typename IndexT, bool WEIGHTED>
+__device__ __forceinline__ StagedBag stage_bag(const KParams& p, uint32_t item, uint32_t end) {
+  StagedBag s;
+  s.valid = 0;
+  s.start = 0;
+  s.L = 0;
+  s.ct = 0;
+  s.b = 0;
+  s.t = 0;
+  if (item < end) {  // wave-uniform; no vector memory access inside
+    TbeTableDesc td;
+    s.valid = item_bag<IndexT>(p, item, td, s.start, s.L, s.ct, s.b, s.t);
+    if (!s.valid) s.L = 0;
+  }
+  const int n = min(s.L, kWave);
+  s.idx = load_index_chunk<IndexT>(p, s.start, n);
+  s.w = WEIGHTED ? load_weight_chunk(p, s.start, n) : 0.f;
+  return s;
+}
+
+// Reduce the R row slots of each element and store the bag's output slice.
+// Slot bits 5 and 4 are reduce-scattered with permlane swaps: each swap+add
+// finishes one element in each half of the lane pair, so after those levels a
+// lane holds E>>k fully-summed elements and every slot stores its share; the
+// slot bits below 4 are summed with DPP row rotations.
+template <int WT, int LG>
+__device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDesc& td, int L, int dw, bool col_ok,
+                                             int64_t b, const float (&acc)[Traits<WT>::kEpd], float bacc) {
   constexpr int E = Traits<WT>::kEpd;
+  constexpr bool HDR = Traits<WT>::kHdr;
+  constexpr bool S5 = LG <= 5 && E >= 2;
+  constexpr int E1 = S5 ? E / 2 : E;
+  constexpr bool S4 = LG <= 4 && E1 >= 2;
+  constexpr int E2 = S4 ? E1 / 2 : E1;
+  const int lane = threadIdx.x & (kWave - 1);
+  float a1[E1];
+  if constexpr (S5) {
+#pragma unroll
+    for (int e = 0; e < E1; ++e) {
+      // lanes 0-31 finish element e, lanes 32-63 element e + E1
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]), __float_as_uint(acc[e + E1]),
+                                                      false, false);
+      a1[e] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E1; ++e) a1[e] = LG <= 5 ? sum_xor32(acc[e]) : acc[e];
+  }
+  float a2[E2];
+  if constexpr (S4) {
+#pragma unroll
+    for (int e = 0; e < E2; ++e) {
+      // even rows of 16 finish element e, odd rows element e + E2
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a1[e]), __float_as_uint(a1[e + E2]),
+                                                      false, false);
+      a2[e] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E2; ++e) a2[e] = LG <= 4 ? sum_xor16(a1[e]) : a1[e];
+  }
+#pragma unroll
+  for (int e = 0; e < E2; ++e) {
+    if constexpr (LG <= 3) a2[e] = add_row_ror<8>(a2[e]);
+    if constexpr (LG <= 2) a2[e] = add_row_ror<4>(a2[e]);
+    if constexpr (LG <= 1) a2[e] = add_row_ror<2>(a2[e]);
+    if constexpr (LG == 0) a2[e] = add_row_ror<1>(a2[e]);
+  }
+  if constexpr (HDR) bacc = sum_slots(bacc, LG);
+
+  // which lanes store: slot bits reduced by butterflies must be zero
+  uint32_t need_zero = 0;
+  if constexpr (LG < 4) need_zero |= (0xFu >> LG) << LG;  // bits [LG, 4)
+  if constexpr (LG <= 4 && !S4) need_zero |= 0x10u;
+  if constexpr (LG <= 5 && !S5) need_zero |= 0x20u;
+  if (!col_ok || (static_cast<uint32_t>(lane) & need_zero)) return;
+  int e0 = 0;
+  if constexpr (S5) e0 += (lane & 32) ? E1 : 0;
+  if constexpr (S4) e0 += (lane & 16) ? E2 : 0;
+  const float scale = (p.mean && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;  // P:355
+  float r[E2];
+#pragma unroll
+  for (int e = 0; e < E2; ++e) {
+    const float x = HDR ? fmaf(a2[e], acc_post_scale<WT>(), bacc) : a2[e];
+    r[e] = p.mean ? x * scale : x;
+  }
+  store_out<E2>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E + e0, r);
+}
+
+// Gather and accumulate the rows of one chunk of <= 64 indices (`idx`: this
+// lane's index, `n` live lanes).  The steps of a chunk are unrolled at compile
+// time and guarded by wave-uniform tests, so each step's loads are issued as
+// straight-line code after the previous step's rows were consumed.
+template <int WT, int LG, bool WEIGHTED>
+__device__ __forceinline__ void pool_chunk(const KParams& p, const __amdgpu_buffer_rsrc_t& rs, uint32_t col,
+                                           uint32_t rows, uint32_t stride, uint64_t idx, float my_w, int n,
+                                           float (&acc)[Traits<WT>::kEpd], float& bacc) {
   constexpr bool HDR = Traits<WT>::kHdr;
   constexpr int R = kWave >> LG;
   constexpr int U = unroll_for<LG>();
+  constexpr int kSteps = kWave / (R * U);
   const int lane = threadIdx.x & (kWave - 1);
-  const int slot = lane >> LG;
-  const int dw = ct * kWave + (lane & ((1 << LG) - 1));
-  const bool col_ok = dw < td.data_dwords;
-  const uint32_t col = static_cast<uint32_t>(td.data_offset + (col_ok ? 4 * dw : 0));
-  const uint32_t rows = static_cast<uint32_t>(td.num_rows);
-  const uint32_t stride = static_cast<uint32_t>(td.row_stride);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(p.weights + td.weights_offset), 0, static_cast<int>(rows * stride), kRsrcWord3);
-  const int slot4 = slot * 4;
-
-  float acc[E];
+  const int slot4 = (lane >> LG) * 4;
+  // each lane turns its index into a byte offset once; rejected indices and
+  // lanes past the chunk get kNoRow
+  const uint32_t my_off = (lane < n && idx < rows) ? static_cast<uint32_t>(idx) * stride : kNoRow;
 #pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  float bacc = 0.f;
-
-  for (int base = 0; base < L; base += kWave) {
-    const int n = min(kWave, L - base);
-    // stage up to 64 indices of the bag with one coalesced load; each lane turns
-    // its index into a byte offset once
-    uint32_t my_off = kNoRow;
-    float my_w = 0.f;
-    if (lane < n) {
-      const int64_t idx = load_index(p, p.indices, start + base + lane);
-      if (static_cast<uint64_t>(idx) < rows) my_off = static_cast<uint32_t>(idx) * stride;
-      if constexpr (WEIGHTED) my_w = p.psw[start + base + lane];
-    }
-    for (int r0 = 0; r0 < n; r0 += R * U) {
+  for (int st = 0; st < kSteps; ++st) {
+    constexpr int kRowsPerStep = R * U;
+    if (st * kRowsPerStep < n) {  // wave-uniform
       uint32_t d[U], h[U];
       float w[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const bool live = r0 + u * R < n;  // wave-uniform
-        // slot r0+u*R+slot < 64 whenever live (R divides 64 and r0+u*R < n <= 64)
-        const int src = ((r0 + u * R) & (kWave - 1)) * 4 + slot4;
-        uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
-        off = live ? off : kNoRow;
+        // slot st*R*U + u*R + slot < 64 (R*U divides 64); slots past n read kNoRow
+        const int src = (st * kRowsPerStep + u * R) * 4 + slot4;
+        const uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
         d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off + col), 0, 0));
         if constexpr (HDR) h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
         else h[u] = 0u;
         if constexpr (WEIGHTED) w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
         else w[u] = 1.f;
       }
+      // keep every load of the step here, ahead of the guarded accumulations
+      // (otherwise the backend may sink a load into the block that consumes it)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (r0 + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, d[u], h[u], w[u], p.fp8);
+        if (st * kRowsPerStep + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, d[u], h[u], w[u], p.fp8);
       }
     }
   }
+}
 
-  reduce_slots<E, HDR>(acc, bacc, LG);
-  if (slot == 0 && col_ok) finish_bag<WT>(p, td, L, dw, b, acc, bacc);
+// One wavefront pools a staged bag over its column tile (P:44-85 bag walk,
+// P:282-315 pooling, P:346-394 chunked bag, P:319-342 store) for a table whose
+// rows span < 2 GiB.
+template <int WT, int LG, typename IndexT, bool WEIGHTED>
+__device__ __forceinline__ void pool_bag_fast(const KParams& p, const StagedBag& sb) {
+  constexpr int E = Traits<WT>::kEpd;
+  static_assert(kWave % ((kWave >> LG) * unroll_for<LG>()) == 0, "a step must not cross a 64-index chunk");
+  const TbeTableDesc td = load_desc(p.tables + sb.t);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int dw = sb.ct * kWave + (lane & ((1 << LG) - 1));
+  const bool col_ok = dw < td.data_dwords;
+  const uint32_t col = static_cast<uint32_t>(td.data_offset + (col_ok ? 4 * dw : 0));
+  const uint32_t rows = static_cast<uint32_t>(td.num_rows);
+  const uint32_t stride = static_cast<uint32_t>(td.row_stride);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.weights + td.weights_offset), 0, static_cast<int>(rows * stride), kRsrcWord3);
+  const int L = sb.L;
+
+  float acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  float bacc = 0.f;
+  // chunk 0 was staged by stage_bag; bags longer than 64 load their later chunks here
+  pool_chunk<WT, LG, WEIGHTED>(p, rs, col, rows, stride, sb.idx, sb.w, min(L, kWave), acc, bacc);
+  for (int base = kWave; base < L; base += kWave) {
+    const int n = min(kWave, L - base);
+    const uint64_t idx = load_index_chunk<IndexT>(p, sb.start + base, n);
+    const float w = WEIGHTED ? load_weight_chunk(p, sb.start + base, n) : 0.f;
+    pool_chunk<WT, LG, WEIGHTED>(p, rs, col, rows, stride, idx, w, n, acc, bacc);
+  }
+  reduce_store<WT, LG>(p, td, L, dw, col_ok, sb.b, acc, bacc);
 }
 
 // ---------------------------------------------------------------- pooled bag, 64-bit tables
@@ -607,29 +778,6 @@ __device__ __forceinline__ void pool_bag_wide(const KParams& p, const TbeTableDe
 
 // ---------------------------------------------------------------- pooled kernels
 
-// Work item -> bag of the group: table, sample, column tile and the bag's index
-// range.  Returns false when the item's column tile does not exist for its table.
-__device__ __forceinline__ bool item_bag(const KParams& p, uint32_t item, TbeTableDesc& td, int64_t& start,
-                                         int& L, int& ct, int64_t& b) {
-  uint32_t k = item;
-  ct = 0;
-  if (p.col_tiles > 1) {
-    k = fast_div(item, p.div_tiles);
-    ct = static_cast<int>(item - k * static_cast<uint32_t>(p.col_tiles));
-  }
-  const uint32_t gt = static_cast<uint32_t>(uniform(static_cast<int>(fast_div(k, p.div_B))));
-  b = static_cast<int64_t>(k - gt * static_cast<uint32_t>(p.B));
-  const int32_t t = p.order ? load_uniform(p.order + p.group_first + gt) : static_cast<int32_t>(gt);
-  td = load_desc(p.tables + t);
-  if (ct >= td.col_tiles) return false;
-  const int64_t bag = static_cast<int64_t>(t) * p.B + b;
-  // clamp to the index array so malformed offsets can never read out of bounds
-  start = min(max(load_offset(p, bag), int64_t(0)), p.num_indices);
-  const int64_t end = min(max(load_offset(p, bag + 1), start), p.num_indices);
-  L = static_cast<int>(end - start);
-  return true;
-}
-
 // Items [first, end) of this wave, stepping by `step`: one contiguous range per
 // XCD, interleaved over the XCD's waves.
 struct WaveItems {
@@ -652,15 +800,16 @@ __device__ __forceinline__ WaveItems wave_items(const KParams& p) {
 }
 
 // Kernel for one group of 32-bit tables with weight type WT and 2^LG lanes per row.
-template <int WT, int LG, bool WEIGHTED>
+// The next item's index chunk is requested before the current bag is pooled.
+template <int WT, int LG, typename IndexT, bool WEIGHTED>
 __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
   const WaveItems w = wave_items(p);
+  if (w.first >= w.end) return;
+  StagedBag next = stage_bag<IndexT, WEIGHTED>(p, w.first, w.end);
   for (uint32_t item = w.first; item < w.end; item += w.step) {
-    TbeTableDesc td;
-    int64_t start, b;
-    int L, ct;
-    if (!item_bag(p, item, td, start, L, ct, b)) continue;
-    pool_bag_fast<WT, LG, WEIGHTED>(p, td, start, L, ct, b);
+    const StagedBag cur = next;
+    next = stage_bag<IndexT, WEIGHTED>(p, item + w.step, w.end);  // past the end: stages nothing
+    if (cur.valid) pool_bag_fast<WT, LG, IndexT, WEIGHTED>(p, cur);
   }
 }
 
@@ -672,7 +821,10 @@ __global__ __launch_bounds__(kBlock) void pooled_wide_kernel(KParams p) {
     TbeTableDesc td;
     int64_t start, b;
     int L, ct;
-    if (!item_bag(p, item, td, start, L, ct, b)) continue;
+    int32_t t;
+    const bool ok = p.index64 ? item_bag<int64_t>(p, item, td, start, L, ct, b, t)
+                              : item_bag<int32_t>(p, item, td, start, L, ct, b, t);
+    if (!ok) continue;
     switch (td.weight_ty) {
       case TBE_TY_INT4: pool_bag_wide<TBE_TY_INT4, WEIGHTED>(p, td, start, L, ct, b); break;
       case TBE_TY_INT8: pool_bag_wide<TBE_TY_INT8, WEIGHTED>(p, td, start, L, ct, b); break;
@@ -814,33 +966,34 @@ FastDiv make_fastdiv(uint32_t d) {
 using KernelFn = void (*)(KParams);
 
 template <int WT, int LG>
-KernelFn fast_kernel_for(bool weighted) {
-  return weighted ? pooled_fast_kernel<WT, LG, true> : pooled_fast_kernel<WT, LG, false>;
+KernelFn fast_kernel_for(bool index64, bool weighted) {
+  if (index64) return weighted ? pooled_fast_kernel<WT, LG, int64_t, true> : pooled_fast_kernel<WT, LG, int64_t, false>;
+  return weighted ? pooled_fast_kernel<WT, LG, int32_t, true> : pooled_fast_kernel<WT, LG, int32_t, false>;
 }
 
 template <int WT>
-KernelFn fast_kernel_lg(int lg, bool weighted) {
+KernelFn fast_kernel_lg(int lg, bool index64, bool weighted) {
   switch (lg) {
-    case 0: return fast_kernel_for<WT, 0>(weighted);
-    case 1: return fast_kernel_for<WT, 1>(weighted);
-    case 2: return fast_kernel_for<WT, 2>(weighted);
-    case 3: return fast_kernel_for<WT, 3>(weighted);
-    case 4: return fast_kernel_for<WT, 4>(weighted);
-    case 5: return fast_kernel_for<WT, 5>(weighted);
-    default: return fast_kernel_for<WT, 6>(weighted);
+    case 0: return fast_kernel_for<WT, 0>(index64, weighted);
+    case 1: return fast_kernel_for<WT, 1>(index64, weighted);
+    case 2: return fast_kernel_for<WT, 2>(index64, weighted);
+    case 3: return fast_kernel_for<WT, 3>(index64, weighted);
+    case 4: return fast_kernel_for<WT, 4>(index64, weighted);
+    case 5: return fast_kernel_for<WT, 5>(index64, weighted);
+    default: return fast_kernel_for<WT, 6>(index64, weighted);
   }
 }
 
-KernelFn pooled_kernel_for(const TbePlanGroup& g, bool weighted) {
+KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted) {
   if (!g.offset32) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
   switch (g.weight_ty) {
-    case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, weighted);
-    case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, weighted);
-    case TBE_TY_BF16: return fast_kernel_lg<TBE_TY_BF16>(g.log2_lanes, weighted);
-    case TBE_TY_FP8:  return fast_kernel_lg<TBE_TY_FP8>(g.log2_lanes, weighted);
-    case TBE_TY_INT8: return fast_kernel_lg<TBE_TY_INT8>(g.log2_lanes, weighted);
-    case TBE_TY_INT4: return fast_kernel_lg<TBE_TY_INT4>(g.log2_lanes, weighted);
-    default:          return fast_kernel_lg<TBE_TY_INT2>(g.log2_lanes, weighted);
+    case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64, weighted);
+    case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64, weighted);
+    case TBE_TY_BF16: return fast_kernel_lg<TBE_TY_BF16>(g.log2_lanes, index64, weighted);
+    case TBE_TY_FP8:  return fast_kernel_lg<TBE_TY_FP8>(g.log2_lanes, index64, weighted);
+    case TBE_TY_INT8: return fast_kernel_lg<TBE_TY_INT8>(g.log2_lanes, index64, weighted);
+    case TBE_TY_INT4: return fast_kernel_lg<TBE_TY_INT4>(g.log2_lanes, index64, weighted);
+    default:          return fast_kernel_lg<TBE_TY_INT2>(g.log2_lanes, index64, weighted);
   }
 }
 
@@ -1063,7 +1216,7 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     p.div_tiles = make_fastdiv(static_cast<uint32_t>(g.col_tiles));
     const int64_t items = static_cast<int64_t>(g.count) * a->B * g.col_tiles;
     p.num_items = static_cast<int32_t>(items);
-    const hipError_t err = launch(pooled_kernel_for(g, weighted), p,
+    const hipError_t err = launch(pooled_kernel_for(g, p.index64 != 0, weighted), p,
                                   (items + kWavesPerBlock - 1) / kWavesPerBlock, true, s);
     if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }
