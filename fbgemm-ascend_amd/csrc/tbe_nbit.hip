@@ -627,82 +627,121 @@ __device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDes
   store_out<E2>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E + e0, r);
 }
 
-// Gather and accumulate the rows of one chunk of <= 64 indices (`idx`: this
-// lane's index, `n` live lanes).  The steps of a chunk are unrolled at compile
-// time and guarded by wave-uniform tests, so each step's loads are issued as
-// straight-line code after the previous step's rows were consumed.
+// What a lane needs to gather rows of one bag's table.
+struct BagCtx {
+  __amdgpu_buffer_rsrc_t rs;  // the table's rows; range = rows * stride bytes
+  TbeTableDesc td;
+  uint32_t col;               // byte offset of this lane's payload word in a row
+  int dw;                     // payload word of this lane
+  bool col_ok;                // that word exists (rows narrower than the lanes)
+};
+
+template <int LG>
+__device__ __forceinline__ BagCtx bag_ctx(const KParams& p, const StagedBag& sb) {
+  BagCtx c;
+  c.td = load_desc(p.tables + sb.t);
+  const int lane = threadIdx.x & (kWave - 1);
+  c.dw = sb.ct * kWave + (lane & ((1 << LG) - 1));
+  c.col_ok = c.dw < c.td.data_dwords;
+  c.col = static_cast<uint32_t>(c.td.data_offset + (c.col_ok ? 4 * c.dw : 0));
+  c.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.weights + c.td.weights_offset), 0,
+                                           static_cast<int>(static_cast<uint32_t>(c.td.num_rows) *
+                                                            static_cast<uint32_t>(c.td.row_stride)),
+                                           kRsrcWord3);
+  return c;
+}
+
+// This lane's index of a chunk as a byte offset into the table (kNoRow for a
+// rejected index or a lane past the chunk's n indices).
+__device__ __forceinline__ uint32_t row_offset(const BagCtx& c, uint64_t idx, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t rows = static_cast<uint32_t>(c.td.num_rows);
+  return (lane < n && idx < rows) ? static_cast<uint32_t>(idx) * static_cast<uint32_t>(c.td.row_stride) : kNoRow;
+}
+
+// Registers of one gather step: U rows per lane slot.
+template <int U>
+struct StepRegs {
+  uint32_t d[U], h[U];
+  float w[U];
+};
+
+// Issue the loads of step `st` of a chunk (rows st*R*U .. st*R*U + R*U - 1).
+// Slot st*R*U + u*R + slot < 64 because R*U divides 64; slots past the chunk
+// read lanes that hold kNoRow and load zero.
 template <int WT, int LG, bool WEIGHTED>
-__device__ __forceinline__ void pool_chunk(const KParams& p, const __amdgpu_buffer_rsrc_t& rs, uint32_t col,
-                                           uint32_t rows, uint32_t stride, uint64_t idx, float my_w, int n,
-                                           float (&acc)[Traits<WT>::kEpd], float& bacc) {
-  constexpr bool HDR = Traits<WT>::kHdr;
+__device__ __forceinline__ void issue_step(const BagCtx& c, uint32_t my_off, float my_w, int st,
+                                           StepRegs<unroll_for<LG>()>& r) {
   constexpr int R = kWave >> LG;
   constexpr int U = unroll_for<LG>();
-  constexpr int kSteps = kWave / (R * U);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int slot4 = (lane >> LG) * 4;
-  // each lane turns its index into a byte offset once; rejected indices and
-  // lanes past the chunk get kNoRow
-  const uint32_t my_off = (lane < n && idx < rows) ? static_cast<uint32_t>(idx) * stride : kNoRow;
+  const int slot4 = ((threadIdx.x & (kWave - 1)) >> LG) * 4;
 #pragma unroll
-  for (int st = 0; st < kSteps; ++st) {
-    constexpr int kRowsPerStep = R * U;
-    if (st * kRowsPerStep < n) {  // wave-uniform
-      uint32_t d[U], h[U];
-      float w[U];
+  for (int u = 0; u < U; ++u) {
+    const int src = (st * R * U + u * R) * 4 + slot4;
+    const uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
+    r.d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(c.rs, static_cast<int>(off + c.col), 0, 0));
+    if constexpr (Traits<WT>::kHdr) r.h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(c.rs, static_cast<int>(off), 0, 0));
+    else r.h[u] = 0u;
+    if constexpr (WEIGHTED) r.w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
+    else r.w[u] = 1.f;
+  }
+}
+
+template <int WT, int LG, bool WEIGHTED>
+__device__ __forceinline__ void consume_step(const KParams& p, const StepRegs<unroll_for<LG>()>& r, int st, int n,
+                                             float (&acc)[Traits<WT>::kEpd], float& bacc) {
+  constexpr int R = kWave >> LG;
+  constexpr int U = unroll_for<LG>();
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        // slot st*R*U + u*R + slot < 64 (R*U divides 64); slots past n read kNoRow
-        const int src = (st * kRowsPerStep + u * R) * 4 + slot4;
-        const uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
-        d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off + col), 0, 0));
-        if constexpr (HDR) h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
-        else h[u] = 0u;
-        if constexpr (WEIGHTED) w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
-        else w[u] = 1.f;
-      }
-      // keep every load of the step here, ahead of the guarded accumulations
-      // (otherwise the backend may sink a load into the block that consumes it)
+  for (int u = 0; u < U; ++u) {
+    if (st * R * U + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, r.d[u], r.h[u], r.w[u], p.fp8);  // wave-uniform
+  }
+}
+
+// Steps st0.. of one chunk of <= 64 indices, each issued then consumed.
+template <int WT, int LG, bool WEIGHTED>
+__device__ __forceinline__ void pool_steps(const KParams& p, const BagCtx& c, uint32_t my_off, float my_w, int n,
+                                           int st0, float (&acc)[Traits<WT>::kEpd], float& bacc) {
+  constexpr int kSteps = kWave / ((kWave >> LG) * unroll_for<LG>());
+#pragma unroll
+  for (int st = 1; st < kSteps; ++st) {
+    if (st >= st0 && st * (kWave / kSteps) < n) {  // wave-uniform
+      StepRegs<unroll_for<LG>()> r;
+      issue_step<WT, LG, WEIGHTED>(c, my_off, my_w, st, r);
+      // keep the step's loads together, ahead of the guarded accumulations
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (st * kRowsPerStep + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, d[u], h[u], w[u], p.fp8);
-      }
+      consume_step<WT, LG, WEIGHTED>(p, r, st, n, acc, bacc);
     }
   }
 }
 
-// One wavefront pools a staged bag over its column tile (P:44-85 bag walk,
-// P:282-315 pooling, P:346-394 chunked bag, P:319-342 store) for a table whose
-// rows span < 2 GiB.
+// Finish a bag whose step 0 rows are in `r0`: consume them, gather the rest of
+// the bag (longer than one step or one chunk), reduce and store (P:44-85 bag
+// walk, P:282-315 pooling, P:346-394 chunked bag, P:319-342 store).
 template <int WT, int LG, typename IndexT, bool WEIGHTED>
-__device__ __forceinline__ void pool_bag_fast(const KParams& p, const StagedBag& sb) {
+__device__ __forceinline__ void finish_bag_fast(const KParams& p, const StagedBag& sb, const BagCtx& c,
+                                                uint32_t my_off, const StepRegs<unroll_for<LG>()>& r0) {
   constexpr int E = Traits<WT>::kEpd;
-  static_assert(kWave % ((kWave >> LG) * unroll_for<LG>()) == 0, "a step must not cross a 64-index chunk");
-  const TbeTableDesc td = load_desc(p.tables + sb.t);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int dw = sb.ct * kWave + (lane & ((1 << LG) - 1));
-  const bool col_ok = dw < td.data_dwords;
-  const uint32_t col = static_cast<uint32_t>(td.data_offset + (col_ok ? 4 * dw : 0));
-  const uint32_t rows = static_cast<uint32_t>(td.num_rows);
-  const uint32_t stride = static_cast<uint32_t>(td.row_stride);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(p.weights + td.weights_offset), 0, static_cast<int>(rows * stride), kRsrcWord3);
-  const int L = sb.L;
-
   float acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
   float bacc = 0.f;
-  // chunk 0 was staged by stage_bag; bags longer than 64 load their later chunks here
-  pool_chunk<WT, LG, WEIGHTED>(p, rs, col, rows, stride, sb.idx, sb.w, min(L, kWave), acc, bacc);
+  const int L = sb.L;
+  const int n0 = min(L, kWave);
+  consume_step<WT, LG, WEIGHTED>(p, r0, 0, n0, acc, bacc);
+  pool_steps<WT, LG, WEIGHTED>(p, c, my_off, sb.w, n0, 1, acc, bacc);
   for (int base = kWave; base < L; base += kWave) {
     const int n = min(kWave, L - base);
     const uint64_t idx = load_index_chunk<IndexT>(p, sb.start + base, n);
     const float w = WEIGHTED ? load_weight_chunk(p, sb.start + base, n) : 0.f;
-    pool_chunk<WT, LG, WEIGHTED>(p, rs, col, rows, stride, idx, w, n, acc, bacc);
+    const uint32_t off = row_offset(c, idx, n);
+    StepRegs<unroll_for<LG>()> r;
+    issue_step<WT, LG, WEIGHTED>(c, off, w, 0, r);
+    __builtin_amdgcn_sched_barrier(0);
+    consume_step<WT, LG, WEIGHTED>(p, r, 0, n, acc, bacc);
+    pool_steps<WT, LG, WEIGHTED>(p, c, off, w, n, 1, acc, bacc);
   }
-  reduce_store<WT, LG>(p, td, L, dw, col_ok, sb.b, acc, bacc);
+  if (sb.valid) reduce_store<WT, LG>(p, c.td, L, c.dw, c.col_ok, sb.b, acc, bacc);
 }
 
 // ---------------------------------------------------------------- pooled bag, 64-bit tables
@@ -800,16 +839,47 @@ __device__ __forceinline__ WaveItems wave_items(const KParams& p) {
 }
 
 // Kernel for one group of 32-bit tables with weight type WT and 2^LG lanes per row.
-// The next item's index chunk is requested before the current bag is pooled.
+// Software pipeline over the wave's items: while bag i is consumed, the rows of
+// bag i+1 are in flight and the index chunk of bag i+2 is being fetched.  The
+// loop body is unrolled twice so the two row buffers swap roles without copies.
 template <int WT, int LG, typename IndexT, bool WEIGHTED>
 __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
+  constexpr int U = unroll_for<LG>();
   const WaveItems w = wave_items(p);
   if (w.first >= w.end) return;
-  StagedBag next = stage_bag<IndexT, WEIGHTED>(p, w.first, w.end);
-  for (uint32_t item = w.first; item < w.end; item += w.step) {
-    const StagedBag cur = next;
-    next = stage_bag<IndexT, WEIGHTED>(p, item + w.step, w.end);  // past the end: stages nothing
-    if (cur.valid) pool_bag_fast<WT, LG, IndexT, WEIGHTED>(p, cur);
+  uint32_t item = w.first;
+  StagedBag s0 = stage_bag<IndexT, WEIGHTED>(p, item, w.end);
+  StagedBag s1 = stage_bag<IndexT, WEIGHTED>(p, item + w.step, w.end);
+  BagCtx c0 = bag_ctx<LG>(p, s0);
+  uint32_t off0 = row_offset(c0, s0.idx, min(s0.L, kWave));
+  StepRegs<U> ra, rb;
+  issue_step<WT, LG, WEIGHTED>(c0, off0, s0.w, 0, ra);
+  while (true) {
+    StagedBag s2 = stage_bag<IndexT, WEIGHTED>(p, item + 2 * w.step, w.end);
+    BagCtx c1 = bag_ctx<LG>(p, s1);
+    uint32_t off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
+    issue_step<WT, LG, WEIGHTED>(c1, off1, s1.w, 0, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_bag_fast<WT, LG, IndexT, WEIGHTED>(p, s0, c0, off0, ra);
+    item += w.step;
+    if (item >= w.end) break;
+    s0 = s1;
+    c0 = c1;
+    off0 = off1;
+    s1 = s2;
+
+    s2 = stage_bag<IndexT, WEIGHTED>(p, item + 2 * w.step, w.end);
+    c1 = bag_ctx<LG>(p, s1);
+    off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
+    issue_step<WT, LG, WEIGHTED>(c1, off1, s1.w, 0, ra);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_bag_fast<WT, LG, IndexT, WEIGHTED>(p, s0, c0, off0, rb);
+    item += w.step;
+    if (item >= w.end) break;
+    s0 = s1;
+    c0 = c1;
+    off0 = off1;
+    s1 = s2;
   }
 }
 
