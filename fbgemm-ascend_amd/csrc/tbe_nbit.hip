@@ -82,6 +82,7 @@ struct Fp8Consts {
   uint32_t h16_shift;  // exponent_bits + 3: body bits -> fp16 exponent/mantissa field
   float h16_scale;     // 2^(15 - bias): fp16 reading of the placed body -> code value
   int32_t h16_ok;      // exponent_bits <= 4: every body fits a finite fp16
+  float one;           // 1.0f (see accum_row)
 };
 
 struct KParams {
@@ -251,12 +252,14 @@ __device__ __forceinline__ void accum_row(float (&acc)[Traits<WT>::kEpd], float&
   constexpr int E = Traits<WT>::kEpd;
   if constexpr (Traits<WT>::kHdr) {
     float s = h16lo(h);
-    float bi = h16hi(h);
     if constexpr (WEIGHTED) {
       s *= w;
-      bi *= w;
+      bacc = fmaf(h16hi(h), w, bacc);
+    } else {
+      // c.one is 1.0f; as an opaque operand it keeps this a single v_fma_mix_f32
+      // reading the bias half of the header in place (no separate convert)
+      bacc = fmaf(h16hi(h), c.one, bacc);
     }
-    bacc += bi;
     if constexpr (WT == TBE_TY_INT8) {
       // halves of p0 hold bytes 0 and 2, of p1 bytes 1 and 3
       const uint32_t p0 = d & 0x00FF00FFu, p1 = (d >> 8) & 0x00FF00FFu;
@@ -1011,6 +1014,7 @@ int bits_of(int ty) {
 
 Fp8Consts make_fp8(int bits, int bias) {
   Fp8Consts c{};
+  c.one = 1.0f;
   if (bits < 1 || bits > 7 || bias < 0 || bias > 120) return c;
   c.shift = static_cast<uint32_t>(bits + 16);
   c.mant_bits = static_cast<uint32_t>(7 - bits);
