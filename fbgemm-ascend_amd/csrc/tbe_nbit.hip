@@ -238,9 +238,13 @@ __device__ __forceinline__ void decode(uint32_t d, float (&v)[Traits<WT>::kEpd],
 // so no conversion instruction is needed and every product is exact in fp32);
 // scaling by a power of two commutes with rounding, so the result equals the
 // plain fp32 sum of scale*q.
+//
+// INT4 words are split with two masks per byte pair (no shift for the odd
+// nibbles), so odd elements arrive as (16q) * 2^-24 and take 2^20 instead.
 template <int WT>
-__device__ __forceinline__ constexpr float acc_post_scale() {
-  return (WT == TBE_TY_INT8 || WT == TBE_TY_INT4 || WT == TBE_TY_INT2) ? 16777216.0f : 1.0f;
+__device__ __forceinline__ float acc_post_scale(int e) {
+  if constexpr (WT == TBE_TY_INT4) return (e & 1) ? 1048576.0f : 16777216.0f;
+  return (WT == TBE_TY_INT8 || WT == TBE_TY_INT2) ? 16777216.0f : 1.0f;
 }
 
 // Add one row's contribution: acc[e] += w * value[e] (value = scale*q + bias for INT
@@ -268,13 +272,18 @@ __device__ __forceinline__ void accum_row(float (&acc)[Traits<WT>::kEpd], float&
       acc[1] = fmaf(h16lo(p1), s, acc[1]);
       acc[3] = fmaf(h16hi(p1), s, acc[3]);
     } else if constexpr (WT == TBE_TY_INT4) {
-      // nibbles j and j+4 of the word are elements j and j+4
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t pj = (d >> (4 * j)) & 0x000F000Fu;
-        acc[j] = fmaf(h16lo(pj), s, acc[j]);
-        acc[j + 4] = fmaf(h16hi(pj), s, acc[j + 4]);
-      }
+      // nibble n of the word is element n; halves of p0..p3 hold elements (0,4),
+      // (1,5) x16, (2,6), (3,7) x16 (see acc_post_scale)
+      const uint32_t d8 = d >> 8;
+      const uint32_t p0 = d & 0x000F000Fu, p1 = d & 0x00F000F0u, p2 = d8 & 0x000F000Fu, p3 = d8 & 0x00F000F0u;
+      acc[0] = fmaf(h16lo(p0), s, acc[0]);
+      acc[4] = fmaf(h16hi(p0), s, acc[4]);
+      acc[1] = fmaf(h16lo(p1), s, acc[1]);
+      acc[5] = fmaf(h16hi(p1), s, acc[5]);
+      acc[2] = fmaf(h16lo(p2), s, acc[2]);
+      acc[6] = fmaf(h16hi(p2), s, acc[6]);
+      acc[3] = fmaf(h16lo(p3), s, acc[3]);
+      acc[7] = fmaf(h16hi(p3), s, acc[7]);
     } else {  // INT2: 2-bit fields j and j+8 are elements j and j+8
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -457,7 +466,7 @@ __device__ __forceinline__ void finish_bag(const KParams& p, const TbeTableDesc&
   float r[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const float x = Traits<WT>::kHdr ? fmaf(acc[e], acc_post_scale<WT>(), bacc) : acc[e];
+    const float x = Traits<WT>::kHdr ? fmaf(acc[e], acc_post_scale<WT>(e), bacc) : acc[e];
     r[e] = p.mean ? x * scale : x;
   }
   store_out<E>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E, r);
@@ -488,6 +497,27 @@ __device__ __forceinline__ bool item_bag(const KParams& p, uint32_t item, TbeTab
   const int64_t end = min(max(static_cast<int64_t>(load_uniform(offs + bag + 1)), start), p.num_indices);
   L = static_cast<int>(end - start);
   return true;
+}
+
+// Items [first, end) of this wave, stepping by `step`: one contiguous range per
+// XCD, interleaved over the XCD's waves.
+struct WaveItems {
+  uint32_t first, end, step;
+};
+
+__device__ __forceinline__ WaveItems wave_items(const KParams& p) {
+  const uint32_t wv = static_cast<uint32_t>(uniform(threadIdx.x >> 6));
+  // every partition must own at least one block
+  const uint32_t nparts = p.xcd ? min(static_cast<uint32_t>(kNumXcd), gridDim.x) : 1u;
+  const uint32_t part = blockIdx.x % nparts;
+  const uint32_t lblk = blockIdx.x / nparts;
+  const uint32_t nblk = (gridDim.x - part + nparts - 1) / nparts;  // blocks of this partition
+  const uint32_t I = static_cast<uint32_t>(p.num_items);
+  WaveItems w;
+  w.first = static_cast<uint32_t>(static_cast<uint64_t>(I) * part / nparts) + lblk * kWavesPerBlock + wv;
+  w.end = static_cast<uint32_t>(static_cast<uint64_t>(I) * (part + 1) / nparts);
+  w.step = nblk * kWavesPerBlock;
+  return w;
 }
 
 // ---------------------------------------------------------------- pooled bag, 32-bit tables
@@ -541,20 +571,71 @@ __device__ __forceinline__ float load_weight_chunk(const KParams& p, int64_t fir
   return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (threadIdx.x & (kWave - 1)) * 4, 0, 0));
 }
 
-template <typename IndexT, bool WEIGHTED>
-__device__ __forceinline__ StagedBag stage_bag(const KParams& p, uint32_t item, uint32_t end) {
-  StagedBag s;
-  s.valid = 0;
-  s.start = 0;
-  s.L = 0;
-  s.ct = 0;
-  s.b = 0;
-  s.t = 0;
-  if (item < end) {  // wave-uniform; no vector memory access inside
-    TbeTableDesc td;
-    s.valid = item_bag<IndexT>(p, item, td, s.start, s.L, s.ct, s.b, s.t);
-    if (!s.valid) s.L = 0;
+// Per-lane bag table: lane l describes item l of the current batch of the wave's
+// items, gathered with vector loads once per 64 items so that no chain of
+// dependent scalar loads (table order -> descriptor -> offsets) sits on the
+// per-bag path.  Requires num_indices < 2^31.
+struct BagTable {
+  int32_t tct;    // table id | column tile << 24, or -1 (no such item / tile)
+  int32_t b;      // sample
+  uint32_t start; // first index position
+  int32_t L;      // bag length
+};
+
+template <typename IndexT>
+__device__ __forceinline__ BagTable load_bag_table(const KParams& p, uint32_t item, bool ok) {
+  BagTable r;
+  r.tct = -1;
+  r.b = 0;
+  r.start = 0;
+  r.L = 0;
+  if (ok) {
+    uint32_t k = item;
+    int ct = 0;
+    if (p.col_tiles > 1) {
+      k = fast_div(item, p.div_tiles);
+      ct = static_cast<int>(item - k * static_cast<uint32_t>(p.col_tiles));
+    }
+    const uint32_t gt = fast_div(k, p.div_B);
+    const int32_t b = static_cast<int32_t>(k - gt * static_cast<uint32_t>(p.B));
+    const int32_t t = p.order[p.group_first + gt];
+    const int tiles = static_cast<int>((reinterpret_cast<const uint32_t*>(p.tables + t)[9] >> 16) & 0xFFu);
+    if (ct < tiles) {
+      const int64_t bag = static_cast<int64_t>(t) * p.B + b;
+      const IndexT* offs = static_cast<const IndexT*>(p.offsets);
+      // clamp to the index array so malformed offsets can never read out of bounds
+      const int64_t start = min(max(static_cast<int64_t>(offs[bag]), int64_t(0)), p.num_indices);
+      const int64_t end = min(max(static_cast<int64_t>(offs[bag + 1]), start), p.num_indices);
+      r.tct = t | (ct << 24);
+      r.b = b;
+      r.start = static_cast<uint32_t>(start);
+      r.L = static_cast<int32_t>(end - start);
+    }
   }
+  return r;
+}
+
+// Stage the wave's item g (items are staged in order g = 0, 1, 2, ...): the bag
+// table is (re)loaded when g starts a new batch of 64.
+template <typename IndexT, bool WEIGHTED>
+__device__ __forceinline__ StagedBag stage_bag(const KParams& p, const WaveItems& w, uint32_t nitems, BagTable& tab,
+                                               uint32_t g) {
+  if ((g & (kWave - 1)) == 0 && g < nitems) {  // wave-uniform
+    const uint32_t l = g + (threadIdx.x & (kWave - 1));
+    tab = load_bag_table<IndexT>(p, w.first + l * w.step, l < nitems);
+  }
+  StagedBag s;
+  // every value goes through readfirstlane: selects on uniform values are
+  // otherwise materialised in VGPRs and the buffer descriptors built from them
+  // become waterfall loops
+  const int kk = static_cast<int>(g & (kWave - 1));
+  const int tct = uniform(g < nitems ? __builtin_amdgcn_readlane(tab.tct, kk) : -1);
+  s.valid = tct >= 0;
+  s.t = uniform(s.valid ? (tct & 0xFFFFFF) : 0);
+  s.ct = uniform(s.valid ? (tct >> 24) : 0);
+  s.b = __builtin_amdgcn_readlane(tab.b, kk);
+  s.start = static_cast<uint32_t>(uniform(s.valid ? __builtin_amdgcn_readlane(static_cast<int>(tab.start), kk) : 0));
+  s.L = uniform(s.valid ? __builtin_amdgcn_readlane(tab.L, kk) : 0);
   const int n = min(s.L, kWave);
   s.idx = load_index_chunk<IndexT>(p, s.start, n);
   s.w = WEIGHTED ? load_weight_chunk(p, s.start, n) : 0.f;
@@ -624,7 +705,7 @@ __device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDes
   float r[E2];
 #pragma unroll
   for (int e = 0; e < E2; ++e) {
-    const float x = HDR ? fmaf(a2[e], acc_post_scale<WT>(), bacc) : a2[e];
+    const float x = HDR ? fmaf(a2[e], acc_post_scale<WT>(e0 + e), bacc) : a2[e];
     r[e] = p.mean ? x * scale : x;
   }
   store_out<E2>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E + e0, r);
@@ -820,26 +901,6 @@ __device__ __forceinline__ void pool_bag_wide(const KParams& p, const TbeTableDe
 
 // ---------------------------------------------------------------- pooled kernels
 
-// Items [first, end) of this wave, stepping by `step`: one contiguous range per
-// XCD, interleaved over the XCD's waves.
-struct WaveItems {
-  uint32_t first, end, step;
-};
-
-__device__ __forceinline__ WaveItems wave_items(const KParams& p) {
-  const uint32_t wv = static_cast<uint32_t>(uniform(threadIdx.x >> 6));
-  // every partition must own at least one block
-  const uint32_t nparts = p.xcd ? min(static_cast<uint32_t>(kNumXcd), gridDim.x) : 1u;
-  const uint32_t part = blockIdx.x % nparts;
-  const uint32_t lblk = blockIdx.x / nparts;
-  const uint32_t nblk = (gridDim.x - part + nparts - 1) / nparts;  // blocks of this partition
-  const uint32_t I = static_cast<uint32_t>(p.num_items);
-  WaveItems w;
-  w.first = static_cast<uint32_t>(static_cast<uint64_t>(I) * part / nparts) + lblk * kWavesPerBlock + wv;
-  w.end = static_cast<uint32_t>(static_cast<uint64_t>(I) * (part + 1) / nparts);
-  w.step = nblk * kWavesPerBlock;
-  return w;
-}
 
 // Kernel for one group of 32-bit tables with weight type WT and 2^LG lanes per row.
 // Software pipeline over the wave's items: while bag i is consumed, the rows of
@@ -850,35 +911,35 @@ __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
   constexpr int U = unroll_for<LG>();
   const WaveItems w = wave_items(p);
   if (w.first >= w.end) return;
-  uint32_t item = w.first;
-  StagedBag s0 = stage_bag<IndexT, WEIGHTED>(p, item, w.end);
-  StagedBag s1 = stage_bag<IndexT, WEIGHTED>(p, item + w.step, w.end);
+  const uint32_t nitems = (w.end - w.first + w.step - 1) / w.step;
+  BagTable tab;
+  uint32_t g = 0;
+  StagedBag s0 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, 0);
+  StagedBag s1 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, 1);
   BagCtx c0 = bag_ctx<LG>(p, s0);
   uint32_t off0 = row_offset(c0, s0.idx, min(s0.L, kWave));
   StepRegs<U> ra, rb;
   issue_step<WT, LG, WEIGHTED>(c0, off0, s0.w, 0, ra);
   while (true) {
-    StagedBag s2 = stage_bag<IndexT, WEIGHTED>(p, item + 2 * w.step, w.end);
+    StagedBag s2 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, g + 2);
     BagCtx c1 = bag_ctx<LG>(p, s1);
     uint32_t off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
     issue_step<WT, LG, WEIGHTED>(c1, off1, s1.w, 0, rb);
     __builtin_amdgcn_sched_barrier(0);
     finish_bag_fast<WT, LG, IndexT, WEIGHTED>(p, s0, c0, off0, ra);
-    item += w.step;
-    if (item >= w.end) break;
+    if (++g >= nitems) break;
     s0 = s1;
     c0 = c1;
     off0 = off1;
     s1 = s2;
 
-    s2 = stage_bag<IndexT, WEIGHTED>(p, item + 2 * w.step, w.end);
+    s2 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, g + 2);
     c1 = bag_ctx<LG>(p, s1);
     off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
     issue_step<WT, LG, WEIGHTED>(c1, off1, s1.w, 0, ra);
     __builtin_amdgcn_sched_barrier(0);
     finish_bag_fast<WT, LG, IndexT, WEIGHTED>(p, s0, c0, off0, rb);
-    item += w.step;
-    if (item >= w.end) break;
+    if (++g >= nitems) break;
     s0 = s1;
     c0 = c1;
     off0 = off1;
@@ -1058,8 +1119,8 @@ KernelFn fast_kernel_lg(int lg, bool index64, bool weighted) {
   }
 }
 
-KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted) {
-  if (!g.offset32) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
+KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted, bool wide) {
+  if (wide || !g.offset32) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
   switch (g.weight_ty) {
     case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64, weighted);
     case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64, weighted);
@@ -1280,6 +1341,8 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
   const TbePlanSummary& plan = *a->plan;
   if (plan.num_groups < 1 || plan.num_groups > TBE_MAX_GROUPS) return fail(TBE_ERR_INVALID_ARG, "bad plan");
   const bool weighted = a->indice_weights != nullptr;
+  // the per-group kernels keep index positions in 32 bits
+  const bool wide = a->num_indices > 0x7FFFFFFF;
   for (int gi = 0; gi < plan.num_groups; ++gi) {
     const TbePlanGroup& g = plan.groups[gi];
     if (g.count <= 0 || g.first < 0 || g.first + g.count > a->T || g.col_tiles < 1 || g.col_tiles > 255)
@@ -1290,7 +1353,7 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     p.div_tiles = make_fastdiv(static_cast<uint32_t>(g.col_tiles));
     const int64_t items = static_cast<int64_t>(g.count) * a->B * g.col_tiles;
     p.num_items = static_cast<int32_t>(items);
-    const hipError_t err = launch(pooled_kernel_for(g, p.index64 != 0, weighted), p,
+    const hipError_t err = launch(pooled_kernel_for(g, p.index64 != 0, weighted, wide), p,
                                   (items + kWavesPerBlock - 1) / kWavesPerBlock, true, s);
     if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }
