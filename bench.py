@@ -41,7 +41,69 @@ def _parse():
                     help="run a plain 1 GiB device copy instead (calibrates rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "tbe_int4_cfg2_traffic.json"),
                     help="HBM traffic per launch measured with rocprofv3 --pmc (JSON)")
+    ap.add_argument("--op", default="tbe", choices=["tbe", "permute_pooled_embs"],
+                    help="tbe: the headline TBE forward; permute_pooled_embs: the pooled-output "
+                         "permutation on config 4's output shape")
     return ap.parse_args()
+
+
+def bench_permute(args, pkg, dev):
+    """permute_pooled_embs on the pooled output of config 4 ([32768, 200 x 128] fp16):
+    a strided column copy, priced as 2 * B * total_D * 2 bytes per call."""
+    import numpy as np
+    import torch
+    import __graft_entry__ as graft
+
+    B, T, D = 32768, 200, 128
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x7BE4)
+    x = torch.randn(B, T * D, device=dev, generator=g).to(torch.float16)
+    perm = torch.randperm(T, device=dev, generator=g)
+    off = torch.arange(0, (T + 1) * D, D, dtype=torch.int64, device=dev)
+    inv = off.clone()
+    inv_perm = torch.argsort(perm)
+    step = lambda: torch.ops.fbgemm.permute_pooled_embs(x, off, perm, inv, inv_perm)  # noqa: E731
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    mean_ms = sum(ms) / len(ms)
+    nbytes = 2 * B * T * D * 2
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        oracle = graft.load_oracle()
+        rows = 2048
+        xs = x[:rows].cpu().view(torch.int16).numpy()
+        offs, perms, invs = off.cpu().numpy(), perm.cpu().numpy(), inv.cpu().numpy()
+        reps, c0 = 0, time.perf_counter()
+        while time.perf_counter() - c0 < args.cpu_seconds and reps < 1000:
+            oracle.permute_pooled_embs(xs, offs, perms, invs)
+            reps += 1
+        el = time.perf_counter() - c0
+        cpu = {"value": 2 * rows * T * D * 2 * reps / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{rows} of {B} rows, {reps} reps in {el:.1f}s, oracle/tbe_oracle.c (1 thread)"}
+    out = {"metric": "permute_pooled_embs achieved HBM GB/s, 1 GPU", "value": achieved, "unit": "GB/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+           "data": "synthetic (seeded, generated on device)",
+           "config": {"workload": "permute_pooled_embs of config 4's pooled output", "batch": B,
+                      "features": T, "D": D, "dtype": "fp16"},
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+           "kernel_ms": mean_ms, "kernel_ms_median": ms[len(ms) // 2], "bytes_per_step": nbytes,
+           "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
 
 
 def _cpu_cores():
@@ -101,6 +163,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.op == "permute_pooled_embs":
+        bench_permute(args, pkg, dev)
+        return
     if args.copy_calibration:
         src = torch.randint(0, 255, (2 ** 30,), dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

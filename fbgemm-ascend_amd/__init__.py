@@ -33,24 +33,42 @@ OP_SCHEMA = (
     "int? fp8_exponent_bits, int? fp8_exponent_bias) -> Tensor"
 )
 
-_schema_lib = None
+# Reference: src/pooled_embedding_ops/permute_pooled_embs/permute_pooled_embs.cpp:107-121
+# (fbgemm_gpu's schema, also exposed in the mxrec namespace).
+PERMUTE_POOLED_EMBS_SCHEMA = (
+    "permute_pooled_embs(Tensor pooled_embs, Tensor offset_dim_list, Tensor permute_list, "
+    "Tensor inv_offset_dim_list, Tensor inv_permute_list) -> Tensor"
+)
+
+# (namespace, op name, schema) of every op this package implements for HIP tensors
+SCHEMAS = [
+    ("fbgemm", OP_NAME, OP_SCHEMA),
+    ("fbgemm", "permute_pooled_embs", PERMUTE_POOLED_EMBS_SCHEMA),
+    ("mxrec", "permute_pooled_embs", PERMUTE_POOLED_EMBS_SCHEMA),
+]
+
+_schema_libs = []
 _loaded = False
 
 
-def _op_defined() -> bool:
+def _op_defined(qualname: str) -> bool:
     try:
-        torch._C._dispatch_find_schema_or_throw("fbgemm::" + OP_NAME, "")
+        torch._C._dispatch_find_schema_or_throw(qualname, "")
         return True
     except RuntimeError:
         return False
 
 
 def _define_schema() -> None:
-    global _schema_lib
-    if _op_defined():
-        return
-    _schema_lib = torch.library.Library("fbgemm", "FRAGMENT")
-    _schema_lib.define(OP_SCHEMA)
+    """Define each schema that no other library (e.g. fbgemm_gpu) has defined."""
+    libs = {}
+    for ns, name, schema in SCHEMAS:
+        if _op_defined(f"{ns}::{name}"):
+            continue
+        if ns not in libs:
+            libs[ns] = torch.library.Library(ns, "FRAGMENT")
+            _schema_libs.append(libs[ns])
+        libs[ns].define(schema)
 
 
 def load_library() -> None:
@@ -74,6 +92,7 @@ load_library()
 from . import capi  # noqa: E402,F401
 from .sparse_types import PoolingMode, SparseType  # noqa: E402,F401
 from .tbe_module import IntNBitTableBatchedEmbeddingBagsCodegen  # noqa: E402,F401
+from .permute_pooled_embedding_modules import PermutePooledEmbeddings  # noqa: E402,F401
 
 
 def int_nbit_split_embedding_codegen_lookup_function(**kwargs):

@@ -1,6 +1,7 @@
 """In-tree build of the HIP library and its torch binding (no cmake, no JIT cache).
 
-  libtbe_hip.so    hand-written gfx950 kernels + the C ABI of include/tbe_nbit.h
+  libtbe_hip.so    hand-written gfx950 kernels + the C ABIs of include/tbe_nbit.h and
+                   include/tbe_pooled_ops.h
   _tbe_torch.so    registers fbgemm::int_nbit_split_embedding_codegen_lookup_function
                    for HIP tensors; links libtbe_hip.so through $ORIGIN
 
@@ -40,9 +41,23 @@ def _run(cmd):
         raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
 
 
+HIP_SOURCES = ["tbe_nbit.hip", "pooled_ops.hip"]
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
+
+
 def build_hip_lib():
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
-          os.path.join(CSRC, "tbe_nbit.hip"), "-o", HIP_LIB])
+    """Compile every HIP source to an object (in parallel), then link one .so."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
+    cmds = [[hipcc, *HIP_FLAGS, "-c", f"-I{INCLUDE}", f"-I{CSRC}", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(HIP_SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        for f in [ex.submit(_run, c) for c in cmds]:
+            f.result()
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", *objs, "-o", HIP_LIB])
 
 
 def build_torch_binding():

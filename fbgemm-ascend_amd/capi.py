@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI declared in include/tbe_nbit.h (libtbe_hip.so).
+"""ctypes binding of the C ABIs declared in include/tbe_nbit.h and
+include/tbe_pooled_ops.h (libtbe_hip.so).
 
 This is the same boundary a cgo/JNI/N-API binding would use; the GPU parity
 tests call the kernels through it directly, without the torch dispatcher.
@@ -13,7 +14,8 @@ import numpy as np
 from . import HIP_LIB
 
 ABI_VERSION = 2
-EXPORTS = ("tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version")
+EXPORTS = ("tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version",
+           "tbe_permute_pooled_embs")
 
 TBE_OK, TBE_ERR_INVALID_ARG, TBE_ERR_UNSUPPORTED, TBE_ERR_LAUNCH = 0, -1, -2, -3
 TBE_FLAG_NO_XCD_REMAP = 0x1
@@ -64,6 +66,14 @@ class TbeNbitArgs(ctypes.Structure):
                 ("output", ctypes.c_void_p), ("output_stride", ctypes.c_int64)]
 
 
+class TbePermutePooledArgs(ctypes.Structure):
+    _fields_ = [("pooled_embs", ctypes.c_void_p), ("output", ctypes.c_void_p),
+                ("B", ctypes.c_int64), ("total_D", ctypes.c_int64), ("inner", ctypes.c_int64),
+                ("elem_size", ctypes.c_int32), ("T", ctypes.c_int32),
+                ("offset_dim_list", ctypes.c_void_p), ("permute_list", ctypes.c_void_p),
+                ("inv_offset_dim_list", ctypes.c_void_p)]
+
+
 _lib = None
 
 
@@ -83,6 +93,8 @@ def lib():
         L.tbe_last_error.argtypes = []
         L.tbe_nbit_abi_version.restype = ctypes.c_int
         L.tbe_nbit_abi_version.argtypes = []
+        L.tbe_permute_pooled_embs.restype = ctypes.c_int
+        L.tbe_permute_pooled_embs.argtypes = [ctypes.POINTER(TbePermutePooledArgs), ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -173,4 +185,29 @@ def forward_tensors(dev_weights, weights_offsets, weights_tys, D_offsets, indice
     stream = torch.cuda.current_stream(dev).cuda_stream
     forward(a, stream)
     out._tbe_keepalive = (tables, order_d)  # the plan arrays must outlive the async launch
+    return out
+
+
+def permute_pooled_embs(pooled_embs, offset_dim_list, permute_list, inv_offset_dim_list, out=None):
+    """tbe_permute_pooled_embs on torch device tensors (the lists: int64 device tensors)."""
+    import torch
+
+    x = pooled_embs.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    a = TbePermutePooledArgs()
+    a.pooled_embs = x.data_ptr()
+    a.output = out.data_ptr()
+    a.B = x.shape[0]
+    a.total_D = x.shape[1]
+    a.inner = x.numel() // max(1, x.shape[0] * x.shape[1])
+    a.elem_size = x.element_size()
+    a.T = permute_list.numel()
+    a.offset_dim_list = offset_dim_list.data_ptr()
+    a.permute_list = permute_list.data_ptr()
+    a.inv_offset_dim_list = inv_offset_dim_list.data_ptr()
+    stream = torch.cuda.current_stream(x.device).cuda_stream if x.is_cuda else 0
+    rc = lib().tbe_permute_pooled_embs(ctypes.byref(a), ctypes.c_void_p(stream))
+    if rc != TBE_OK:
+        raise TbeError(rc, last_error())
     return out

@@ -51,6 +51,7 @@
 #include <utility>
 #include <vector>
 
+#include "tbe_internal.h"
 #include "tbe_nbit.h"
 
 namespace tbe {
@@ -1051,7 +1052,8 @@ __global__ __launch_bounds__(kBlock) void nobag_kernel(KParams p) {
 
 thread_local std::string g_last_error;
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error() { g_last_error.clear(); }
+
 int fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;

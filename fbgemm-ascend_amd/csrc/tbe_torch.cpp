@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "tbe_nbit.h"
+#include "tbe_pooled_ops.h"
 
 namespace tbe_torch {
 
@@ -234,10 +235,67 @@ Tensor int_nbit_split_embedding_codegen_lookup_function_hip(
   return output;
 }
 
+// Reference: src/pooled_embedding_ops/permute_pooled_embs/permute_pooled_embs.cpp
+// ("PA"), checks of PA:25-60 with the same messages.  inv_permute_list is not used
+// (PA:69).  Unlike PA:82-98 the host never reads the lists (no synchronisation):
+// every segment is copied on the device.
+Tensor permute_pooled_embs_hip(const Tensor& pooled_embs, const Tensor& offset_dim_list,
+                               const Tensor& permute_list, const Tensor& inv_offset_dim_list,
+                               const Tensor& inv_permute_list) {
+  (void)inv_permute_list;
+  TORCH_CHECK(pooled_embs.dim() >= 2, "pooled_embs must be at least 2-D");
+  TORCH_CHECK(offset_dim_list.scalar_type() == at::kLong, "offset_dim_list must be int64");
+  TORCH_CHECK(permute_list.scalar_type() == at::kLong, "permute_list must be int64");
+  TORCH_CHECK(inv_offset_dim_list.scalar_type() == at::kLong, "inv_offset_dim_list must be int64");
+  const int64_t T = permute_list.numel();
+  TORCH_CHECK(offset_dim_list.numel() == T + 1, "offset_dim_list must have T+1 elements");
+  TORCH_CHECK(inv_offset_dim_list.numel() == T + 1, "inv_offset_dim_list must have T+1 elements");
+  const auto st = pooled_embs.scalar_type();
+  TORCH_CHECK(st == at::kFloat || st == at::kHalf || st == at::kBFloat16,
+              "pooled_embs must be float32, float16, or bfloat16");
+  const std::vector<std::pair<const Tensor*, const char*>> all = {
+      {&pooled_embs, "pooled_embs"}, {&offset_dim_list, "offset_dim_list"},
+      {&permute_list, "permute_list"}, {&inv_offset_dim_list, "inv_offset_dim_list"}};
+  for (const auto& [x, name] : all) {
+    TORCH_CHECK(x->defined(), name, " tensor must be defined");
+    TORCH_CHECK(x->numel() > 0, name, " tensor must be non-empty");
+    TORCH_CHECK(x->dim() > 0, name, " tensor must have non-zero dimensions");
+    TORCH_CHECK(x->is_cuda() && x->get_device() == pooled_embs.get_device(), name,
+                " must be on the same HIP device as pooled_embs");
+  }
+  at::OptionalDeviceGuard guard(at::device_of(pooled_embs));
+  const Tensor in = pooled_embs.contiguous();
+  const Tensor off = offset_dim_list.contiguous();
+  const Tensor perm = permute_list.contiguous();
+  const Tensor inv = inv_offset_dim_list.contiguous();
+  Tensor output = at::empty_like(in);
+  TbePermutePooledArgs a{};
+  a.pooled_embs = in.data_ptr();
+  a.output = output.data_ptr();
+  a.B = in.size(0);
+  a.total_D = in.size(1);
+  a.inner = in.numel() / std::max<int64_t>(1, a.B * a.total_D);
+  a.elem_size = static_cast<int32_t>(in.element_size());
+  a.T = static_cast<int32_t>(T);
+  a.offset_dim_list = off.data_ptr<int64_t>();
+  a.permute_list = perm.data_ptr<int64_t>();
+  a.inv_offset_dim_list = inv.data_ptr<int64_t>();
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(in.get_device()).stream();
+  const int rc = tbe_permute_pooled_embs(&a, stream);
+  TORCH_CHECK(rc == TBE_OK, "permute_pooled_embs: ", tbe_last_error());
+  return output;
+}
+
 }  // namespace tbe_torch
 
 // PyTorch-ROCm routes HIP tensors through the CUDA dispatch key.
 TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("int_nbit_split_embedding_codegen_lookup_function",
          TORCH_FN(tbe_torch::int_nbit_split_embedding_codegen_lookup_function_hip));
+  m.impl("permute_pooled_embs", TORCH_FN(tbe_torch::permute_pooled_embs_hip));  // PA:119-121
+}
+
+// PA:107-117: the reference also exposes the op as mxrec::permute_pooled_embs.
+TORCH_LIBRARY_IMPL(mxrec, CUDA, m) {
+  m.impl("permute_pooled_embs", TORCH_FN(tbe_torch::permute_pooled_embs_hip));
 }

@@ -46,6 +46,8 @@ def lib():
             getattr(L, name).argtypes = [P, P, i64]
         L.oracle_row_stride.restype = i64
         L.oracle_row_stride.argtypes = [ctypes.c_int, i64, i64]
+        L.oracle_permute_pooled_embs.restype = None
+        L.oracle_permute_pooled_embs.argtypes = [P, P, i64, i64, i64, ctypes.c_int, ctypes.c_int, P, P, P]
         _lib = L
     return _lib
 
@@ -134,3 +136,23 @@ def forward(dev_weights, weights_offsets, weights_tys, D_offsets, indices, offse
     if rc != 0:
         raise ValueError("oracle_tbe_forward rejected its arguments")
     return out, out_f32
+
+
+def permute_pooled_embs(pooled_embs: np.ndarray, offset_dim_list, permute_list, inv_offset_dim_list,
+                        out: np.ndarray | None = None) -> np.ndarray:
+    """CPU restatement of permute_pooled_embs (oracle_permute_pooled_embs in tbe_oracle.c).
+    `pooled_embs` is any [B, total_D, ...] array of 2- or 4-byte elements; the result
+    has the same dtype and bits.  Columns no segment writes are taken from `out`
+    (zeros by default)."""
+    x = np.ascontiguousarray(pooled_embs)
+    if x.itemsize not in (2, 4) or x.ndim < 2:
+        raise TypeError("pooled_embs must be at least 2-D with 2- or 4-byte elements")
+    off = np.ascontiguousarray(offset_dim_list, dtype=np.int64)
+    perm = np.ascontiguousarray(permute_list, dtype=np.int64)
+    inv = np.ascontiguousarray(inv_offset_dim_list, dtype=np.int64)
+    res = np.zeros_like(x) if out is None else np.ascontiguousarray(out, dtype=x.dtype).copy()
+    B, D = x.shape[0], x.shape[1]
+    inner = x.size // max(1, B * D)
+    lib().oracle_permute_pooled_embs(_ptr(x), _ptr(res), B, D, inner, x.itemsize, len(perm),
+                                     _ptr(off), _ptr(perm), _ptr(inv))
+    return res

@@ -278,3 +278,38 @@ void oracle_float_to_half_n(const float* in, uint16_t* out, int64_t n) {
 void oracle_float_to_bf16_n(const float* in, uint16_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = oracle_float_to_bf16(in[i]);
 }
+
+/*
+ * permute_pooled_embs: output[:, inv[i] : inv[i+1]] = input[:, off[p] : off[p] + that
+ * width], p = perm[i], for i in [0, T) (reference permute_pooled_embs.cpp:83-98,
+ * the host path that builds the column list and index_selects dim 1, and the
+ * kernel's segment walk permute_pooled_embs_kernel.h:173-211).  Rows are
+ * [total_D, inner] elements of `es` bytes.  Beyond the reference (which does not
+ * check these on its device path): a destination segment with p outside [0, T) or
+ * source columns outside [0, total_D) is zero-filled; one whose own columns leave
+ * [0, total_D) is left untouched.
+ */
+void oracle_permute_pooled_embs(const uint8_t* in, uint8_t* out, int64_t B, int64_t total_D, int64_t inner,
+                                int es, int T, const int64_t* off, const int64_t* perm, const int64_t* inv) {
+  const int64_t cb = inner * es;
+  const int64_t rb = total_D * cb;
+  for (int i = 0; i < T; ++i) {
+    const int64_t dst = inv[i], dst_end = inv[i + 1];
+    if (dst < 0 || dst_end < dst || dst_end > total_D) continue;
+    const int64_t len = dst_end - dst;
+    const int64_t p = perm[i];
+    int zero = p < 0 || p >= T;
+    int64_t src = 0;
+    if (!zero) {
+      src = off[p];
+      zero = src < 0 || src + len > total_D;
+    }
+    for (int64_t b = 0; b < B; ++b) {
+      uint8_t* o = out + b * rb + dst * cb;
+      if (zero)
+        memset(o, 0, (size_t)(len * cb));
+      else
+        memcpy(o, in + b * rb + src * cb, (size_t)(len * cb));
+    }
+  }
+}

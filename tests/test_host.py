@@ -14,9 +14,14 @@ FP32, FP16, INT8, INT4, INT2, BF16, FP8 = 0, 1, 2, 3, 4, 5, 6
 
 
 def _header_functions():
-    text = open(os.path.join(ROOT, "include", "tbe_nbit.h")).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(tbe_\w+)\s*\(", text, flags=re.M)))
+    names = set()
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not h.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(tbe_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
 
 
 def test_abi_exports_every_declared_symbol(pkg):
@@ -24,7 +29,7 @@ def test_abi_exports_every_declared_symbol(pkg):
     assert {"tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version"} <= set(names)
     lib = ctypes.CDLL(pkg.HIP_LIB)
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in include/tbe_nbit.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     assert set(names) == set(pkg.capi.EXPORTS)
 
 
@@ -33,8 +38,10 @@ def test_abi_version_and_struct_layout(pkg, tmp_path):
     import subprocess
     c = pkg.capi
     assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 2
-    structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanGroup, c.TbePlanSummary, c.TbeNbitArgs]
-    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tbe_nbit.h"', "int main(void){"]
+    structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanGroup, c.TbePlanSummary, c.TbeNbitArgs,
+               c.TbePermutePooledArgs]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tbe_nbit.h"', '#include "tbe_pooled_ops.h"',
+             "int main(void){"]
     for st in structs:
         lines.append(f'printf("%zu\\n", sizeof({st.__name__}));')
         for f, _ in st._fields_:
