@@ -41,9 +41,10 @@ def _parse():
                     help="run a plain 1 GiB device copy instead (calibrates rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "tbe_int4_cfg2_traffic.json"),
                     help="HBM traffic per launch measured with rocprofv3 --pmc (JSON)")
-    ap.add_argument("--op", default="tbe", choices=["tbe", "permute_pooled_embs"],
+    ap.add_argument("--op", default="tbe", choices=["tbe", "permute_pooled_embs", "block_bucketize_sparse_features"],
                     help="tbe: the headline TBE forward; permute_pooled_embs: the pooled-output "
-                         "permutation on config 4's output shape")
+                         "permutation on config 4's output shape; block_bucketize_sparse_features: the "
+                         "reference's stress case (16 features x 8192 samples, 128-512 indices, my_size 16)")
     return ap.parse_args()
 
 
@@ -149,6 +150,67 @@ def cpu_baseline(wl, target_s: float):
                       f"oracle/tbe_oracle.c OpenMP fp32"}
 
 
+def bench_bucketize(args, pkg, dev):
+    """block_bucketize_sparse_features on the reference's i64_stress perf case, priced at the
+    op's unavoidable bytes: indices read once and written once, lengths read, new_lengths written."""
+    import numpy as np
+    import torch
+    import __graft_entry__ as graft
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _bucketize_cases import CASES, gen_case
+
+    case = [c for c in CASES if c.name == "i64_stress"][0]
+    lengths, indices, block_sizes, _ = gen_case(case, 0x7BE5)
+    L_d, I_d, B_d = (torch.from_numpy(a).to(dev) for a in (lengths, indices, block_sizes))
+    op = torch.ops.fbgemm.block_bucketize_sparse_features
+    step = lambda: op(L_d, I_d, False, False, B_d, case.my_size)  # noqa: E731
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    mean_ms = sum(ms) / len(ms)
+    N, L = indices.size, lengths.size
+    nbytes = 2 * N * indices.itemsize + L * lengths.itemsize + case.my_size * L * lengths.itemsize
+    cpu = None
+    if not args.no_cpu_baseline:
+        oracle = graft.load_oracle()
+        rows = L // 16
+        n_s = int(lengths[:rows].sum())
+        reps, c0 = 0, time.perf_counter()
+        while time.perf_counter() - c0 < args.cpu_seconds and reps < 1000:
+            oracle.block_bucketize_sparse_features(lengths[:rows], indices[:n_s], False, False, block_sizes,
+                                                   case.my_size)
+            reps += 1
+        el = time.perf_counter() - c0
+        cpu = {"value": n_s * reps / el, "unit": "indices/s", "cores": 1, "kind": "port",
+               "sample": f"first {rows} of {L} rows ({n_s} indices), {reps} reps in {el:.1f}s, "
+                         "oracle/tbe_oracle.c (1 thread)"}
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    out = {"metric": "block_bucketize_sparse_features indices/s, 1 GPU", "value": N / (mean_ms * 1e-3),
+           "unit": "indices/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int64", "data": "synthetic (seeded)",
+           "config": {"workload": "reference perf case i64_stress", "features": case.num_features,
+                      "batch": case.batch_size, "lengths": [case.min_length, case.max_length],
+                      "my_size": case.my_size, "num_indices": int(N)},
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+           "kernel_ms": mean_ms, "kernel_ms_median": ms[len(ms) // 2], "bytes_per_step": nbytes,
+           "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -165,6 +227,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.op == "permute_pooled_embs":
         bench_permute(args, pkg, dev)
+        return
+    if args.op == "block_bucketize_sparse_features":
+        bench_bucketize(args, pkg, dev)
         return
     if args.copy_calibration:
         src = torch.randint(0, 255, (2 ** 30,), dtype=torch.uint8, device=dev)

@@ -40,11 +40,21 @@ PERMUTE_POOLED_EMBS_SCHEMA = (
     "Tensor inv_offset_dim_list, Tensor inv_permute_list) -> Tensor"
 )
 
+# Reference: src/sparse_ops/block_bucketize_sparse_features/block_bucketize_sparse_features.cpp:248-254
+BLOCK_BUCKETIZE_SCHEMA = (
+    "block_bucketize_sparse_features(Tensor lengths, Tensor indices, bool bucketize_pos, bool sequence, "
+    "Tensor block_sizes, SymInt my_size, Tensor? weights=None, Tensor? batch_size_per_feature=None, "
+    "SymInt max_B= -1, Tensor[]? block_bucketize_pos=None, bool keep_orig_idx=False, "
+    "Tensor? total_num_blocks=None) -> (Tensor, Tensor, Tensor?, Tensor?, Tensor?)"
+)
+
 # (namespace, op name, schema) of every op this package implements for HIP tensors
 SCHEMAS = [
     ("fbgemm", OP_NAME, OP_SCHEMA),
     ("fbgemm", "permute_pooled_embs", PERMUTE_POOLED_EMBS_SCHEMA),
     ("mxrec", "permute_pooled_embs", PERMUTE_POOLED_EMBS_SCHEMA),
+    ("fbgemm", "block_bucketize_sparse_features", BLOCK_BUCKETIZE_SCHEMA),
+    ("mxrec", "block_bucketize_sparse_features", BLOCK_BUCKETIZE_SCHEMA),
 ]
 
 _schema_libs = []

@@ -1,7 +1,7 @@
 """In-tree build of the HIP library and its torch binding (no cmake, no JIT cache).
 
-  libtbe_hip.so    hand-written gfx950 kernels + the C ABIs of include/tbe_nbit.h and
-                   include/tbe_pooled_ops.h
+  libtbe_hip.so    hand-written gfx950 kernels + the C ABIs of include/tbe_nbit.h,
+                   include/tbe_pooled_ops.h and include/tbe_sparse_ops.h
   _tbe_torch.so    registers fbgemm::int_nbit_split_embedding_codegen_lookup_function
                    for HIP tensors; links libtbe_hip.so through $ORIGIN
 
@@ -41,7 +41,7 @@ def _run(cmd):
         raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
 
 
-HIP_SOURCES = ["tbe_nbit.hip", "pooled_ops.hip"]
+HIP_SOURCES = ["tbe_nbit.hip", "pooled_ops.hip", "sparse_ops.hip"]
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 
 

@@ -1,5 +1,5 @@
-"""ctypes binding of the C ABIs declared in include/tbe_nbit.h and
-include/tbe_pooled_ops.h (libtbe_hip.so).
+"""ctypes binding of the C ABIs declared in include/tbe_nbit.h,
+include/tbe_pooled_ops.h and include/tbe_sparse_ops.h (libtbe_hip.so).
 
 This is the same boundary a cgo/JNI/N-API binding would use; the GPU parity
 tests call the kernels through it directly, without the torch dispatcher.
@@ -15,7 +15,8 @@ from . import HIP_LIB
 
 ABI_VERSION = 2
 EXPORTS = ("tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version",
-           "tbe_permute_pooled_embs")
+           "tbe_permute_pooled_embs", "tbe_block_bucketize_workspace_bytes",
+           "tbe_block_bucketize_sparse_features")
 
 TBE_OK, TBE_ERR_INVALID_ARG, TBE_ERR_UNSUPPORTED, TBE_ERR_LAUNCH = 0, -1, -2, -3
 TBE_FLAG_NO_XCD_REMAP = 0x1
@@ -74,6 +75,21 @@ class TbePermutePooledArgs(ctypes.Structure):
                 ("inv_offset_dim_list", ctypes.c_void_p)]
 
 
+class TbeBlockBucketizeArgs(ctypes.Structure):
+    _fields_ = [("indices", ctypes.c_void_p), ("num_indices", ctypes.c_int64),
+                ("offsets", ctypes.c_void_p), ("lengths_size", ctypes.c_int64),
+                ("index_size", ctypes.c_int32), ("offset_size", ctypes.c_int32),
+                ("block_sizes", ctypes.c_void_p), ("num_features", ctypes.c_int32),
+                ("keep_orig_idx", ctypes.c_int32), ("my_size", ctypes.c_int64),
+                ("weights", ctypes.c_void_p), ("batch_size_offsets", ctypes.c_void_p),
+                ("total_num_blocks", ctypes.c_void_p), ("bucketize_pos", ctypes.c_void_p),
+                ("bucketize_pos_len", ctypes.c_void_p), ("new_lengths", ctypes.c_void_p),
+                ("new_offsets", ctypes.c_void_p), ("new_indices", ctypes.c_void_p),
+                ("new_weights", ctypes.c_void_p), ("new_pos", ctypes.c_void_p),
+                ("unbucketize_permute", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_int64)]
+
+
 _lib = None
 
 
@@ -95,6 +111,10 @@ def lib():
         L.tbe_nbit_abi_version.argtypes = []
         L.tbe_permute_pooled_embs.restype = ctypes.c_int
         L.tbe_permute_pooled_embs.argtypes = [ctypes.POINTER(TbePermutePooledArgs), ctypes.c_void_p]
+        L.tbe_block_bucketize_workspace_bytes.restype = ctypes.c_int64
+        L.tbe_block_bucketize_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]
+        L.tbe_block_bucketize_sparse_features.restype = ctypes.c_int
+        L.tbe_block_bucketize_sparse_features.argtypes = [ctypes.POINTER(TbeBlockBucketizeArgs), ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -211,3 +231,52 @@ def permute_pooled_embs(pooled_embs, offset_dim_list, permute_list, inv_offset_d
     if rc != TBE_OK:
         raise TbeError(rc, last_error())
     return out
+
+
+def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, block_sizes, my_size,
+                                    weights=None, batch_size_per_feature=None, block_bucketize_pos=None,
+                                    keep_orig_idx=False, total_num_blocks=None):
+    """tbe_block_bucketize_sparse_features on torch device tensors; returns the op's
+    five outputs (None where not requested) plus new_offsets."""
+    import torch
+
+    dev = indices.device
+    L, N, F = lengths.numel(), indices.numel(), block_sizes.numel()
+    lopt = dict(dtype=lengths.dtype, device=dev)
+    offsets = torch.cumsum(lengths, 0, dtype=lengths.dtype).contiguous()
+    bso = None
+    if batch_size_per_feature is not None:
+        bso = torch.cat([torch.zeros(1, **lopt),
+                         torch.cumsum(batch_size_per_feature, 0, dtype=lengths.dtype)]).contiguous()
+    new_lengths = torch.empty(my_size * L, **lopt)
+    new_offsets = torch.empty(my_size * L + 1, **lopt)
+    new_indices = torch.empty(N, dtype=indices.dtype, device=dev)
+    new_w = torch.empty(N, dtype=torch.float32, device=dev) if weights is not None else None
+    new_pos = torch.empty_like(new_indices) if bucketize_pos else None
+    unb = torch.empty_like(new_indices) if sequence else None
+    keep = [offsets, bso]
+    pos_ptrs = pos_lens = None
+    if block_bucketize_pos is not None:
+        ps = [p.contiguous() for p in block_bucketize_pos]
+        keep += ps
+        pos_ptrs = torch.tensor([p.data_ptr() for p in ps], dtype=torch.int64, device=dev)
+        pos_lens = torch.tensor([p.numel() for p in ps], dtype=torch.int64, device=dev)
+    wsb = lib().tbe_block_bucketize_workspace_bytes(my_size, L, lengths.element_size())
+    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    a = TbeBlockBucketizeArgs()
+    ptr = lambda x: x.data_ptr() if x is not None else None  # noqa: E731
+    a.indices, a.num_indices, a.offsets, a.lengths_size = ptr(indices), N, ptr(offsets), L
+    a.index_size, a.offset_size = indices.element_size(), lengths.element_size()
+    a.block_sizes, a.num_features, a.keep_orig_idx, a.my_size = ptr(block_sizes), F, int(keep_orig_idx), my_size
+    a.weights, a.batch_size_offsets = ptr(weights), ptr(bso)
+    a.total_num_blocks, a.bucketize_pos, a.bucketize_pos_len = ptr(total_num_blocks), ptr(pos_ptrs), ptr(pos_lens)
+    a.new_lengths, a.new_offsets, a.new_indices = ptr(new_lengths), ptr(new_offsets), ptr(new_indices)
+    a.new_weights, a.new_pos, a.unbucketize_permute = ptr(new_w), ptr(new_pos), ptr(unb)
+    a.workspace, a.workspace_bytes = ptr(ws), wsb
+    stream = torch.cuda.current_stream(dev).cuda_stream if indices.is_cuda else 0
+    rc = lib().tbe_block_bucketize_sparse_features(ctypes.byref(a), ctypes.c_void_p(stream))
+    if rc != TBE_OK:
+        raise TbeError(rc, last_error())
+    torch.cuda.synchronize(dev)  # the temporaries above must outlive the launches
+    del keep, ws, pos_ptrs, pos_lens
+    return (new_lengths, new_indices, new_w, new_pos, unb), new_offsets

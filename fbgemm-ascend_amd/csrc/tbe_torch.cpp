@@ -18,6 +18,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <limits>
 #include <list>
 #include <memory>
 #include <mutex>
@@ -26,6 +27,7 @@
 
 #include "tbe_nbit.h"
 #include "tbe_pooled_ops.h"
+#include "tbe_sparse_ops.h"
 
 namespace tbe_torch {
 
@@ -286,6 +288,136 @@ Tensor permute_pooled_embs_hip(const Tensor& pooled_embs, const Tensor& offset_d
   return output;
 }
 
+// Reference: src/sparse_ops/block_bucketize_sparse_features/block_bucketize_sparse_features.cpp
+// ("BA"): the checks of BA:37-91 and BA:107-128 with the same messages, the
+// output allocation of BA:154-204, the offsets of BA:167 and BA:172.
+std::tuple<Tensor, Tensor, c10::optional<Tensor>, c10::optional<Tensor>, c10::optional<Tensor>>
+block_bucketize_sparse_features_hip(const Tensor& lengths, const Tensor& indices, bool bucketize_pos, bool sequence,
+                                    const Tensor& block_sizes, int64_t my_size,
+                                    const c10::optional<Tensor>& weights,
+                                    const c10::optional<Tensor>& batch_size_per_feature, int64_t max_B,
+                                    const c10::optional<std::vector<Tensor>>& block_bucketize_pos,
+                                    bool keep_orig_idx, const c10::optional<Tensor>& total_num_blocks) {
+  TORCH_CHECK(my_size > 0, "my_size must be positive.");
+  if (lengths.scalar_type() == at::kInt)
+    TORCH_CHECK(my_size <= static_cast<int64_t>(std::numeric_limits<uint32_t>::max()),
+                "my_size must fit into uint32 for int32 tensors.");
+  TORCH_CHECK(lengths.dim() == 1, "lengths must be 1D.");
+  TORCH_CHECK(indices.dim() == 1, "indices must be 1D.");
+  TORCH_CHECK(block_sizes.dim() == 1, "block_sizes must be 1D.");
+  TORCH_CHECK(block_sizes.numel() > 0, "block_sizes must be non-empty.");
+  TORCH_CHECK(block_sizes.scalar_type() == indices.scalar_type(), "block_sizes dtype must match indices.");
+  TORCH_CHECK(lengths.scalar_type() == at::kInt || lengths.scalar_type() == at::kLong,
+              "lengths must be int32 or int64.");
+  TORCH_CHECK(indices.scalar_type() == at::kInt || indices.scalar_type() == at::kLong,
+              "indices must be int32 or int64.");
+  if (weights.has_value()) {
+    TORCH_CHECK(weights->dim() == 1, "weights must be 1D.");
+    TORCH_CHECK(weights->numel() == indices.numel(), "weights must match indices length.");
+    TORCH_CHECK(weights->scalar_type() == at::kFloat, "weights dtype must be float32.");
+  }
+  if (batch_size_per_feature.has_value()) {
+    TORCH_CHECK(batch_size_per_feature->dim() == 1, "batch_size_per_feature must be 1D.");
+    TORCH_CHECK(batch_size_per_feature->scalar_type() == lengths.scalar_type(),
+                "batch_size_per_feature dtype must match lengths.");
+    TORCH_CHECK(batch_size_per_feature->numel() == block_sizes.numel(),
+                "batch_size_per_feature length must match block_sizes length.");
+    TORCH_CHECK(max_B > 0, "max_B must be positive when batch_size_per_feature is provided.");
+  } else {
+    TORCH_CHECK(lengths.numel() % block_sizes.numel() == 0,
+                "lengths.size(0) must be divisible by block_sizes.size(0) when batch_size_per_feature is absent.");
+  }
+  if (total_num_blocks.has_value()) {
+    TORCH_CHECK(total_num_blocks->dim() == 1, "total_num_blocks must be 1D.");
+    TORCH_CHECK(total_num_blocks->scalar_type() == indices.scalar_type(),
+                "total_num_blocks dtype must match indices.");
+    TORCH_CHECK(total_num_blocks->numel() == block_sizes.numel(), "total_num_blocks must match block_sizes length.");
+  }
+  const int dev = lengths.get_device();
+  std::vector<std::pair<const Tensor*, const char*>> all = {
+      {&lengths, "lengths"}, {&indices, "indices"}, {&block_sizes, "block_sizes"}};
+  if (weights.has_value()) all.push_back({&*weights, "weights"});
+  if (batch_size_per_feature.has_value()) all.push_back({&*batch_size_per_feature, "batch_size_per_feature"});
+  if (total_num_blocks.has_value()) all.push_back({&*total_num_blocks, "total_num_blocks"});
+  for (const auto& [x, name] : all)
+    TORCH_CHECK(x->is_cuda() && x->get_device() == dev, name, " must be on the same HIP device as lengths");
+
+  at::OptionalDeviceGuard guard(at::device_of(lengths));
+  const Tensor len_c = lengths.contiguous();
+  const Tensor idx_c = indices.contiguous();
+  const Tensor bs_c = block_sizes.contiguous();
+  const int64_t L = len_c.numel();
+  const int64_t N = idx_c.numel();
+  const int64_t F = bs_c.numel();
+  const auto lopt = len_c.options();
+  const auto iopt = idx_c.options();
+  Tensor new_lengths = at::empty({my_size * L}, lopt);
+  Tensor new_offsets = at::empty({my_size * L + 1}, lopt);
+  Tensor new_indices = at::empty({N}, iopt);
+  Tensor offsets = at::cumsum(len_c, 0, len_c.scalar_type()).contiguous();  // BA:167
+  Tensor bso;
+  if (batch_size_per_feature.has_value())  // BA:172: complete cumsum
+    bso = at::cat({at::zeros({1}, lopt), at::cumsum(batch_size_per_feature->contiguous(), 0, len_c.scalar_type())}).contiguous();
+  Tensor w_c, new_w, new_pos, unb, tnb_c, pos_ptrs, pos_lens;
+  std::vector<Tensor> pos_keep;
+  if (weights.has_value()) {
+    w_c = weights->contiguous();
+    new_w = at::empty({N}, w_c.options());
+  }
+  if (bucketize_pos) new_pos = at::empty({N}, iopt);
+  if (sequence) unb = at::empty({N}, iopt);
+  if (total_num_blocks.has_value()) tnb_c = total_num_blocks->contiguous();
+  if (block_bucketize_pos.has_value()) {
+    TORCH_CHECK(static_cast<int64_t>(block_bucketize_pos->size()) == F,
+                "block_bucketize_pos must hold one tensor per feature");
+    std::vector<int64_t> ptrs(F), lens(F);
+    for (int64_t f = 0; f < F; ++f) {
+      const Tensor& t = (*block_bucketize_pos)[f];
+      TORCH_CHECK(t.scalar_type() == idx_c.scalar_type(), "block_bucketize_pos dtype must match indices.");
+      TORCH_CHECK(t.is_cuda() && t.get_device() == dev, "block_bucketize_pos must be on the same HIP device");
+      pos_keep.push_back(t.contiguous());
+      ptrs[f] = reinterpret_cast<int64_t>(pos_keep.back().data_ptr());
+      lens[f] = t.dim() == 1 ? t.numel() : 0;
+    }
+    auto cpu64 = at::TensorOptions().dtype(at::kLong);
+    pos_ptrs = at::tensor(ptrs, cpu64).to(len_c.device());
+    pos_lens = at::tensor(lens, cpu64).to(len_c.device());
+  }
+  const int64_t ws_bytes = tbe_block_bucketize_workspace_bytes(my_size, L, static_cast<int32_t>(len_c.element_size()));
+  TORCH_CHECK(ws_bytes > 0, "block_bucketize_sparse_features: bad sizes");
+  Tensor ws = at::empty({ws_bytes}, lopt.dtype(at::kByte));
+
+  TbeBlockBucketizeArgs a{};
+  a.indices = idx_c.data_ptr();
+  a.num_indices = N;
+  a.offsets = offsets.data_ptr();
+  a.lengths_size = L;
+  a.index_size = static_cast<int32_t>(idx_c.element_size());
+  a.offset_size = static_cast<int32_t>(len_c.element_size());
+  a.block_sizes = bs_c.data_ptr();
+  a.num_features = static_cast<int32_t>(F);
+  a.keep_orig_idx = keep_orig_idx ? 1 : 0;
+  a.my_size = my_size;
+  a.weights = w_c.defined() ? w_c.data_ptr<float>() : nullptr;
+  a.batch_size_offsets = bso.defined() ? bso.data_ptr() : nullptr;
+  a.total_num_blocks = tnb_c.defined() ? tnb_c.data_ptr() : nullptr;
+  a.bucketize_pos = pos_ptrs.defined() ? reinterpret_cast<const void* const*>(pos_ptrs.data_ptr()) : nullptr;
+  a.bucketize_pos_len = pos_lens.defined() ? pos_lens.data_ptr<int64_t>() : nullptr;
+  a.new_lengths = new_lengths.data_ptr();
+  a.new_offsets = new_offsets.data_ptr();
+  a.new_indices = new_indices.data_ptr();
+  a.new_weights = new_w.defined() ? new_w.data_ptr<float>() : nullptr;
+  a.new_pos = new_pos.defined() ? new_pos.data_ptr() : nullptr;
+  a.unbucketize_permute = unb.defined() ? unb.data_ptr() : nullptr;
+  a.workspace = ws.data_ptr();
+  a.workspace_bytes = ws_bytes;
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(dev).stream();
+  const int rc = tbe_block_bucketize_sparse_features(&a, stream);
+  TORCH_CHECK(rc == TBE_OK, "block_bucketize_sparse_features: ", tbe_last_error());
+  auto opt = [](const Tensor& t) { return t.defined() ? c10::optional<Tensor>(t) : c10::nullopt; };
+  return {new_lengths, new_indices, opt(new_w), opt(new_pos), opt(unb)};
+}
+
 }  // namespace tbe_torch
 
 // PyTorch-ROCm routes HIP tensors through the CUDA dispatch key.
@@ -293,9 +425,11 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("int_nbit_split_embedding_codegen_lookup_function",
          TORCH_FN(tbe_torch::int_nbit_split_embedding_codegen_lookup_function_hip));
   m.impl("permute_pooled_embs", TORCH_FN(tbe_torch::permute_pooled_embs_hip));  // PA:119-121
+  m.impl("block_bucketize_sparse_features", TORCH_FN(tbe_torch::block_bucketize_sparse_features_hip));  // BA:262-266
 }
 
 // PA:107-117: the reference also exposes the op as mxrec::permute_pooled_embs.
 TORCH_LIBRARY_IMPL(mxrec, CUDA, m) {
   m.impl("permute_pooled_embs", TORCH_FN(tbe_torch::permute_pooled_embs_hip));
+  m.impl("block_bucketize_sparse_features", TORCH_FN(tbe_torch::block_bucketize_sparse_features_hip));  // BA:256-260
 }

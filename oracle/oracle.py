@@ -46,6 +46,9 @@ def lib():
             getattr(L, name).argtypes = [P, P, i64]
         L.oracle_row_stride.restype = i64
         L.oracle_row_stride.argtypes = [ctypes.c_int, i64, i64]
+        L.oracle_block_bucketize.restype = ctypes.c_int
+        L.oracle_block_bucketize.argtypes = [P, i64, ctypes.c_int, P, ctypes.c_int, i64, P, ctypes.c_int, i64, P, P, P,
+                                             P, P, ctypes.c_int, P, P, P, P, P, P]
         L.oracle_permute_pooled_embs.restype = None
         L.oracle_permute_pooled_embs.argtypes = [P, P, i64, i64, i64, ctypes.c_int, ctypes.c_int, P, P, P]
         _lib = L
@@ -156,3 +159,49 @@ def permute_pooled_embs(pooled_embs: np.ndarray, offset_dim_list, permute_list, 
     lib().oracle_permute_pooled_embs(_ptr(x), _ptr(res), B, D, inner, x.itemsize, len(perm),
                                      _ptr(off), _ptr(perm), _ptr(inv))
     return res
+
+
+def block_bucketize_sparse_features(lengths, indices, bucketize_pos: bool, sequence: bool, block_sizes,
+                                    my_size: int, weights=None, batch_size_per_feature=None,
+                                    block_bucketize_pos=None, keep_orig_idx: bool = False,
+                                    total_num_blocks=None):
+    """CPU restatement of block_bucketize_sparse_features (oracle_block_bucketize in
+    tbe_oracle.c) with the op's argument list; numpy arrays in, a tuple (new_lengths,
+    new_indices, new_weights, new_pos, unbucketize_permute) out, optional entries None
+    when not requested.  Within a (bucket, row) segment indices keep their row order."""
+    L_ = np.ascontiguousarray(lengths)
+    idx = np.ascontiguousarray(indices)
+    bs = np.ascontiguousarray(block_sizes, dtype=idx.dtype)
+    if L_.dtype not in (np.int32, np.int64) or idx.dtype not in (np.int32, np.int64):
+        raise TypeError("lengths and indices must be int32 or int64")
+    os_, is_ = L_.itemsize, idx.itemsize
+    L = L_.size
+    F = bs.size
+    offsets = np.cumsum(L_, dtype=L_.dtype) if L else np.zeros(0, L_.dtype)
+    bso = None
+    if batch_size_per_feature is not None:
+        bso = np.concatenate([[0], np.cumsum(np.asarray(batch_size_per_feature, dtype=np.int64))]).astype(L_.dtype)
+    tnb = None if total_num_blocks is None else np.ascontiguousarray(total_num_blocks, dtype=idx.dtype)
+    pos_arrays = None
+    pos_ptrs = pos_lens = None
+    if block_bucketize_pos is not None:
+        pos_arrays = [np.ascontiguousarray(p, dtype=idx.dtype) for p in block_bucketize_pos]
+        pos_ptrs = (ctypes.c_void_p * F)(*[p.ctypes.data for p in pos_arrays])
+        pos_lens = np.array([p.size for p in pos_arrays], dtype=np.int64)
+    w = None if weights is None else np.ascontiguousarray(weights, dtype=np.float32)
+    new_lengths = np.zeros(my_size * L, dtype=L_.dtype)
+    f = lib().oracle_block_bucketize
+    args_common = [_ptr(idx), idx.size, is_, _ptr(offsets), os_, L, _ptr(bs), F, int(my_size), _ptr(w), _ptr(bso), _ptr(tnb),
+                   pos_ptrs, _ptr(pos_lens), int(bool(keep_orig_idx))]
+    if f(*args_common, _ptr(new_lengths), None, None, None, None, None) != 0:
+        raise MemoryError("oracle_block_bucketize")
+    new_offsets = np.concatenate([[0], np.cumsum(new_lengths.astype(np.int64))]).astype(L_.dtype)
+    n = idx.size
+    new_indices = np.zeros(n, dtype=idx.dtype)
+    new_weights = np.zeros(n, dtype=np.float32) if w is not None else None
+    new_pos = np.zeros(n, dtype=idx.dtype) if bucketize_pos else None
+    unb = np.zeros(n, dtype=idx.dtype) if sequence else None
+    if f(*args_common, _ptr(new_lengths), _ptr(new_offsets), _ptr(new_indices), _ptr(new_weights), _ptr(new_pos),
+         _ptr(unb)) != 0:
+        raise MemoryError("oracle_block_bucketize")
+    return new_lengths, new_indices, new_weights, new_pos, unb

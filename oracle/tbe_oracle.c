@@ -28,6 +28,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 enum { TY_FP32 = 0, TY_FP16 = 1, TY_INT8 = 2, TY_INT4 = 3, TY_INT2 = 4, TY_BF16 = 5, TY_FP8 = 6 };
@@ -312,4 +313,125 @@ void oracle_permute_pooled_embs(const uint8_t* in, uint8_t* out, int64_t B, int6
         memcpy(o, in + b * rb + src * cb, (size_t)(len * cb));
     }
   }
+}
+
+/*
+ * block_bucketize_sparse_features (reference
+ * src/sparse_ops/block_bucketize_sparse_features/block_bucketize_sparse_features.cpp:93-246
+ * and c310/op_kernel/block_bucketize_sparse_features_kernel_full.h: bucket rule 387-455,
+ * new index rule 560-603, sequential write cursor 730-760).
+ *
+ * Row r of `offsets` (inclusive cumsum of lengths, L rows) belongs to feature
+ * r / (L / F), or with batch_size_offsets (complete cumsum of
+ * batch_size_per_feature, F+1 entries) to the last f with bso[f] <= r.  Each index
+ * of the row goes to a bucket in [0, my_size) and is written, in row order, to
+ * segment (bucket, r) of the output, which starts at new_offsets[bucket*L + r]
+ * (new_offsets = complete cumsum of new_lengths).  Index widths: `is` (indices,
+ * block_sizes, total_num_blocks, pos lists), `os` (offsets, new_lengths,
+ * batch_size_offsets), 4 or 8 bytes.  Rows of a feature with a negative block
+ * size, and indices whose bucket would be >= my_size (possible only with
+ * total_num_blocks not a multiple of my_size), are left out (the reference writes
+ * those out of bounds).  Pass new_lengths only (new_indices NULL) to count.
+ */
+static int64_t ld_i(const void* p, int64_t i, int sz) {
+  return sz == 8 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
+}
+static void st_i(void* p, int64_t i, int sz, int64_t v) {
+  if (sz == 8) ((int64_t*)p)[i] = v; else ((int32_t*)p)[i] = (int32_t)v;
+}
+
+static int bb_feature(int64_t r, int64_t L, int F, const void* bso, int os) {
+  if (!bso) {
+    const int64_t B = L / F;
+    return (int)(r / (B > 0 ? B : 1));
+  }
+  int lo = 0, hi = F;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (ld_i(bso, mid, os) <= r) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+/* bucket and new index of one index value; returns 0 if the index is left out */
+static int bb_map(uint64_t u, int is, int64_t blk, int64_t gb, int64_t lbk, uint64_t my, int keep,
+                  const void* pos, int64_t pos_len, int64_t* bucket, int64_t* nidx) {
+  if (is == 4) u = (uint32_t)u;
+  const uint64_t mask = is == 4 ? 0xFFFFFFFFull : ~0ull;
+  if (pos && pos_len > 0) {
+    uint64_t adj = u;
+    if (blk == 0 && gb > 0) {
+      const uint64_t scalar = ((uint64_t)ld_i(pos, pos_len - 1, is) & mask) / (uint64_t)gb;
+      adj = ((u % (uint64_t)gb) * scalar) & mask;
+    }
+    int64_t first = 0, last = pos_len;
+    while (first < last) {
+      const int64_t mid = first + ((last - first) >> 1);
+      if (((uint64_t)ld_i(pos, mid, is) & mask) <= adj) first = mid + 1; else last = mid;
+    }
+    const int64_t lb = first - 1;
+    *bucket = (lb >= 0 && (uint64_t)lb < my) ? lb : (int64_t)(u % my);
+    if (keep) *nidx = (int64_t)u;
+    else if (blk == 0 && gb > 0) *nidx = (int64_t)(u / (uint64_t)gb);
+    else if (lb >= 0 && (uint64_t)lb < my) *nidx = (int64_t)((u - ((uint64_t)ld_i(pos, lb, is) & mask)) & mask);
+    else *nidx = (int64_t)(u / my);
+  } else {
+    const uint64_t gsize = ((uint64_t)blk * (uint64_t)gb) & mask, lsize = ((uint64_t)blk * (uint64_t)lbk) & mask;
+    if (blk != 0 && u < gsize) {
+      *bucket = (int64_t)(u / lsize);
+      *nidx = keep ? (int64_t)u : (int64_t)(u % lsize);
+    } else {
+      *bucket = (int64_t)((u % (uint64_t)gb) / (uint64_t)lbk);
+      *nidx = keep ? (int64_t)u : (int64_t)(u / (uint64_t)gb);
+    }
+  }
+  return (uint64_t)*bucket < my;
+}
+
+int oracle_block_bucketize(const void* indices, int64_t n, int is, const void* offsets, int os, int64_t L,
+                           const void* block_sizes, int F, int64_t my_size, const float* weights,
+                           const void* bso, const void* tnb, const void* const* pos, const int64_t* pos_len,
+                           int keep, void* new_lengths, const void* new_offsets, void* new_indices,
+                           float* new_weights, void* new_pos, void* unbucketize_permute) {
+  int64_t* cursor = NULL;
+  if (new_indices) {
+    cursor = (int64_t*)malloc(sizeof(int64_t) * (size_t)(my_size * L));
+    if (!cursor) return -1;
+    for (int64_t k = 0; k < my_size * L; ++k) cursor[k] = ld_i(new_offsets, k, os);
+  } else {
+    for (int64_t k = 0; k < my_size * L; ++k) st_i(new_lengths, k, os, 0);
+  }
+  for (int64_t r = 0; r < L; ++r) {
+    const int f = bb_feature(r, L, F, bso, os);
+    if (f < 0 || f >= F) continue;
+    const int64_t blk = ld_i(block_sizes, f, is);
+    if (blk < 0) continue;
+    int64_t gb = tnb ? ld_i(tnb, f, is) : my_size;
+    if (gb <= 0) gb = my_size;
+    int64_t lbk = tnb ? gb / my_size : 1;
+    if (lbk <= 0) lbk = 1;
+    const void* pp = pos ? pos[f] : NULL;
+    const int64_t pl = pos ? pos_len[f] : 0;
+    int64_t s = r == 0 ? 0 : ld_i(offsets, r - 1, os), e = ld_i(offsets, r, os);
+    /* clamp to the index array so malformed offsets never read out of bounds */
+    s = s < 0 ? 0 : (s > n ? n : s);
+    e = e < s ? s : (e > n ? n : e);
+    for (int64_t i = s; i < e; ++i) {
+      int64_t b, v;
+      if (!bb_map((uint64_t)ld_i(indices, i, is), is, blk, gb, lbk, (uint64_t)my_size, keep, pp, pl, &b, &v))
+        continue;
+      const int64_t slot = b * L + r;
+      if (!new_indices) {
+        st_i(new_lengths, slot, os, ld_i(new_lengths, slot, os) + 1);
+        continue;
+      }
+      const int64_t w = cursor[slot]++;
+      st_i(new_indices, w, is, v);
+      if (new_weights) new_weights[w] = weights[i];
+      if (new_pos) st_i(new_pos, w, is, i - s);
+      if (unbucketize_permute) st_i(unbucketize_permute, i, is, w);
+    }
+  }
+  free(cursor);
+  return 0;
 }

@@ -1,0 +1,132 @@
+"""GPU parity of block_bucketize_sparse_features: the HIP kernels (through
+torch.ops.fbgemm / torch.ops.mxrec and through the C ABI) against the CPU oracle,
+exactly (integer outputs and copied weights), on the reference test's case list and
+option grid (reference bench/sparse/block_bucketize_sparse_features_test/
+test_block_bucketize_sparse_features_perf.py:96-198: weights x bucketize_pos x
+sequence x keep_orig_idx, total_num_blocks rand/multiple, batch_size_per_feature with
+max_B, block_bucketize_pos).  Outputs are compared in full order: both sides keep
+row order inside every segment."""
+import itertools
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from _bucketize_cases import CASES, gen_batch_size_per_feature, gen_bucketize_pos, gen_case, gen_total_num_blocks
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(oracle, gpu, case, seed, *, weights=False, bucketize_pos=False, sequence=False, keep=False, tnb=None,
+           bspf=False, pos=False, via="fbgemm"):
+    lengths, indices, block_sizes, w = gen_case(case, seed, weights)
+    kw = {}
+    if tnb:
+        kw["total_num_blocks"] = gen_total_num_blocks(block_sizes, case.my_size, tnb, seed)
+    max_B = -1
+    if bspf:
+        kw["batch_size_per_feature"], max_B = gen_batch_size_per_feature(case.num_features, case.batch_size,
+                                                                         lengths.dtype, seed)
+    if pos:
+        kw["block_bucketize_pos"] = gen_bucketize_pos(block_sizes, case.my_size, seed)
+    print(f"[gpu] block_bucketize {case.name} seed={seed} w={weights} pos={bucketize_pos} seq={sequence} "
+          f"keep={keep} tnb={tnb} bspf={bspf} poslist={pos} via={via} N={indices.size}", flush=True)
+    want = oracle.block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, block_sizes,
+                                                  case.my_size, weights=w, keep_orig_idx=keep, **kw)
+    d = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    if via == "capi":
+        from fbgemm_ascend_amd import capi
+        got, _ = capi.block_bucketize_sparse_features(
+            d(lengths), d(indices), bucketize_pos, sequence, d(block_sizes), case.my_size, weights=d(w),
+            batch_size_per_feature=d(kw.get("batch_size_per_feature")),
+            block_bucketize_pos=None if not pos else [d(p) for p in kw["block_bucketize_pos"]],
+            keep_orig_idx=keep, total_num_blocks=d(kw.get("total_num_blocks")))
+    else:
+        op = getattr(torch.ops, via).block_bucketize_sparse_features
+        got = op(d(lengths), d(indices), bucketize_pos, sequence, d(block_sizes), case.my_size, weights=d(w),
+                 batch_size_per_feature=d(kw.get("batch_size_per_feature")), max_B=max_B,
+                 block_bucketize_pos=None if not pos else [d(p) for p in kw["block_bucketize_pos"]],
+                 keep_orig_idx=keep, total_num_blocks=d(kw.get("total_num_blocks")))
+        torch.cuda.synchronize()
+    names = ["new_lengths", "new_indices", "new_weights", "new_pos", "unbucketize_permute"]
+    for name, g, e in zip(names, got, want):
+        if e is None:
+            assert g is None, name
+            continue
+        g = g.cpu().numpy()
+        assert g.dtype == e.dtype, name
+        assert np.array_equal(g, e), f"{name} differs"
+
+
+OPTIONS = list(itertools.product([False, True], repeat=4))  # weights, bucketize_pos, sequence, keep
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
+@pytest.mark.parametrize("opt", [OPTIONS[0], OPTIONS[5], OPTIONS[10], OPTIONS[15]],
+                         ids=lambda o: "w%d_p%d_s%d_k%d" % o)
+def test_bucketize_options(pkg, oracle, gpu, case, opt):
+    w, bp, seq, keep = opt
+    _check(oracle, gpu, case, zlib.crc32(case.name.encode()) % 10000, weights=w, bucketize_pos=bp, sequence=seq,
+           keep=keep)
+
+
+@pytest.mark.parametrize("opt", OPTIONS, ids=lambda o: "w%d_p%d_s%d_k%d" % o)
+def test_bucketize_full_option_grid(pkg, oracle, gpu, opt):
+    w, bp, seq, keep = opt
+    _check(oracle, gpu, CASES[9], 77, weights=w, bucketize_pos=bp, sequence=seq, keep=keep)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
+@pytest.mark.parametrize("tnb", ["rand", "multiple"])
+def test_bucketize_total_num_blocks(pkg, oracle, gpu, case, tnb):
+    _check(oracle, gpu, case, 11, tnb=tnb)
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c.batch_size > 1], ids=lambda c: c.name)
+def test_bucketize_batch_size_per_feature(pkg, oracle, gpu, case):
+    _check(oracle, gpu, case, 13, bspf=True, sequence=True)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
+def test_bucketize_pos_lists(pkg, oracle, gpu, case):
+    _check(oracle, gpu, case, 17, pos=True, sequence=True, bucketize_pos=True)
+
+
+@pytest.mark.parametrize("via", ["mxrec", "capi"])
+def test_bucketize_entry_points(pkg, oracle, gpu, via):
+    _check(oracle, gpu, CASES[1], 19, weights=True, bucketize_pos=True, sequence=True, via=via)
+
+
+def test_bucketize_mixed_dtypes(pkg, oracle, gpu):
+    # int64 lengths with int32 indices and the reverse
+    lengths = np.array([3, 0, 2, 4], np.int64)
+    indices = np.array([1, 9, 17, 4, 30, 2, 3, 25, 8], np.int32)
+    bs = np.array([4, 8], np.int32)
+    for L_, I_ in ((lengths, indices), (lengths.astype(np.int32), indices.astype(np.int64))):
+        want = oracle.block_bucketize_sparse_features(L_, I_, True, True, bs.astype(I_.dtype), 3)
+        got = torch.ops.fbgemm.block_bucketize_sparse_features(
+            torch.from_numpy(L_).to(gpu), torch.from_numpy(I_).to(gpu), True, True,
+            torch.from_numpy(bs.astype(I_.dtype)).to(gpu), 3)
+        for g, e in zip(got, want):
+            if e is not None:
+                assert np.array_equal(g.cpu().numpy(), e)
+
+
+def test_bucketize_empty_inputs(pkg, oracle, gpu):
+    lengths = np.zeros(6, np.int32)
+    indices = np.zeros(0, np.int32)
+    got = torch.ops.fbgemm.block_bucketize_sparse_features(
+        torch.from_numpy(lengths).to(gpu), torch.from_numpy(indices).to(gpu), False, True,
+        torch.tensor([3, 5], dtype=torch.int32, device=gpu), 4)
+    assert got[0].cpu().tolist() == [0] * 24 and got[1].numel() == 0 and got[4].numel() == 0
+
+
+@pytest.mark.parametrize("my_size", [63, 64, 65, 200])
+@pytest.mark.parametrize("sequence", [False, True])
+def test_bucketize_my_size_paths(pkg, oracle, gpu, my_size, sequence):
+    # my_size <= 64 keeps counters in registers, above that in memory with atomics
+    from _bucketize_cases import Case
+    case = Case(f"my{my_size}", 6, 50, 0, 150, 3, 9, my_size, np.int64)
+    _check(oracle, gpu, case, my_size, weights=True, bucketize_pos=True, sequence=sequence)
+    _check(oracle, gpu, case, my_size + 1, tnb="rand", sequence=sequence)

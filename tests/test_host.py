@@ -39,9 +39,9 @@ def test_abi_version_and_struct_layout(pkg, tmp_path):
     c = pkg.capi
     assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 2
     structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanGroup, c.TbePlanSummary, c.TbeNbitArgs,
-               c.TbePermutePooledArgs]
+               c.TbePermutePooledArgs, c.TbeBlockBucketizeArgs]
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tbe_nbit.h"', '#include "tbe_pooled_ops.h"',
-             "int main(void){"]
+             '#include "tbe_sparse_ops.h"', "int main(void){"]
     for st in structs:
         lines.append(f'printf("%zu\\n", sizeof({st.__name__}));')
         for f, _ in st._fields_:
