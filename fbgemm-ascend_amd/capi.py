@@ -13,14 +13,17 @@ import numpy as np
 
 from . import HIP_LIB
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 EXPORTS = ("tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version",
            "tbe_permute_pooled_embs", "tbe_block_bucketize_workspace_bytes",
            "tbe_block_bucketize_sparse_features")
 
 TBE_OK, TBE_ERR_INVALID_ARG, TBE_ERR_UNSUPPORTED, TBE_ERR_LAUNCH = 0, -1, -2, -3
 TBE_FLAG_NO_XCD_REMAP = 0x1
+TBE_FLAG_NO_STREAM = 0x2
+TBE_FLAG_FORCE_STREAM = 0x4
 TBE_TABLE_OFFSET32 = 0x1
+TBE_TABLE_STREAM = 0x2
 
 
 class TbeTableDesc(ctypes.Structure):
@@ -42,7 +45,7 @@ class TbePlanInput(ctypes.Structure):
 class TbePlanGroup(ctypes.Structure):
     _fields_ = [("weight_ty", ctypes.c_int32), ("log2_lanes", ctypes.c_int32),
                 ("offset32", ctypes.c_int32), ("first", ctypes.c_int32), ("count", ctypes.c_int32),
-                ("col_tiles", ctypes.c_int32)]
+                ("col_tiles", ctypes.c_int32), ("stream", ctypes.c_int32)]
 
 
 TBE_MAX_GROUPS = 64
@@ -166,6 +169,18 @@ def forward_tensors(dev_weights, weights_offsets, weights_tys, D_offsets, indice
     """Run the op through the C ABI on torch device tensors (plan + upload + launch).
 
     Allocates the output with torch (zero-filled) unless `out` is given."""
+    return prepare_forward(dev_weights, weights_offsets, weights_tys, D_offsets, indices, offsets, pooling_mode,
+                           indice_weights, output_dtype, row_alignment, fp8_exponent_bits, fp8_exponent_bias,
+                           flags, out)()
+
+
+def prepare_forward(dev_weights, weights_offsets, weights_tys, D_offsets, indices, offsets,
+                    pooling_mode: int, indice_weights=None, output_dtype: int = 0,
+                    row_alignment: int = 16, fp8_exponent_bits: int = -1,
+                    fp8_exponent_bias: int = -1, flags: int = 0, out=None):
+    """Plan, upload the plan and allocate the output once; returns a callable that
+    launches the forward through the C ABI on the current stream and returns the
+    output tensor (the same tensor on every call)."""
     import torch
 
     wo = weights_offsets.detach().cpu().numpy()
@@ -202,10 +217,12 @@ def forward_tensors(dev_weights, weights_offsets, weights_tys, D_offsets, indice
     a.flags = int(flags)
     a.output = out.data_ptr()
     a.output_stride = out.shape[1]
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    forward(a, stream)
-    out._tbe_keepalive = (tables, order_d)  # the plan arrays must outlive the async launch
-    return out
+    out._tbe_keepalive = (tables, order_d)  # the plan arrays must outlive the async launches
+
+    def launch():
+        forward(a, torch.cuda.current_stream(dev).cuda_stream)
+        return out
+    return launch
 
 
 def permute_pooled_embs(pooled_embs, offset_dim_list, permute_list, inv_offset_dim_list, out=None):

@@ -1,0 +1,10 @@
+// tbe_kern_fp16.hip — pooled TBE kernels for FP16, BF16 rows (per-bag and
+// row-stream variants); compiled separately so the library builds in parallel.
+#include "tbe_kernels.h"
+
+namespace tbe {
+template KernelFn fast_kernel_lg<TBE_TY_FP16>(int, bool, bool);
+template KernelFn stream_kernel_lg<TBE_TY_FP16>(int, bool, bool);
+template KernelFn fast_kernel_lg<TBE_TY_BF16>(int, bool, bool);
+template KernelFn stream_kernel_lg<TBE_TY_BF16>(int, bool, bool);
+}  // namespace tbe

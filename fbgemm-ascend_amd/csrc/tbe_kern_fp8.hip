@@ -1,0 +1,8 @@
+// tbe_kern_fp8.hip — pooled TBE kernels for FP8 rows (per-bag and
+// row-stream variants); compiled separately so the library builds in parallel.
+#include "tbe_kernels.h"
+
+namespace tbe {
+template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool);
+template KernelFn stream_kernel_lg<TBE_TY_FP8>(int, bool, bool);
+}  // namespace tbe

@@ -1,0 +1,8 @@
+// tbe_kern_int4.hip — pooled TBE kernels for INT4 rows (per-bag and
+// row-stream variants); compiled separately so the library builds in parallel.
+#include "tbe_kernels.h"
+
+namespace tbe {
+template KernelFn fast_kernel_lg<TBE_TY_INT4>(int, bool, bool);
+template KernelFn stream_kernel_lg<TBE_TY_INT4>(int, bool, bool);
+}  // namespace tbe

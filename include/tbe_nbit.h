@@ -75,6 +75,10 @@ typedef struct TbeTableDesc {
 /* TbeTableDesc.flags: the table's rows span < 2 GiB, so the kernels address them
  * with 32-bit offsets from the table base (buffer loads with range checking). */
 #define TBE_TABLE_OFFSET32 0x1
+/* TbeTableDesc.flags: OFFSET32 and a payload of at least 8 words in an even
+ * number of words, so the table is gathered by the row-stream kernel (8-byte
+ * lanes, one contiguous index run per slot of lanes). */
+#define TBE_TABLE_STREAM 0x2
 
 /* Host-side table metadata handed to the planner (all host pointers). */
 typedef struct TbePlanInput {
@@ -99,6 +103,7 @@ typedef struct TbePlanGroup {
   int32_t first;          /* position in table_order                               */
   int32_t count;          /* tables in the group                                   */
   int32_t col_tiles;      /* max col_tiles over the group's tables                 */
+  int32_t stream;         /* 1: every table has TBE_TABLE_STREAM                   */
 } TbePlanGroup;
 
 #define TBE_MAX_GROUPS 64
@@ -149,6 +154,8 @@ typedef struct TbeNbitArgs {
 
 /* Tuning switches for TbeNbitArgs.flags (results are identical either way). */
 #define TBE_FLAG_NO_XCD_REMAP 0x1  /* keep the hardware's round-robin block order */
+#define TBE_FLAG_NO_STREAM 0x2     /* never use the row-stream kernel (per-bag kernel for every group) */
+#define TBE_FLAG_FORCE_STREAM 0x4  /* row-stream kernel for every eligible group, whatever its size */
 
 /*
  * Validate the table metadata and fill descs[T], table_order[T] (host memory)
@@ -171,7 +178,7 @@ const char* tbe_last_error(void);
 
 /* ABI version of this header; bumped on any layout change of the structs above. */
 int tbe_nbit_abi_version(void);
-#define TBE_NBIT_ABI_VERSION 2
+#define TBE_NBIT_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

@@ -34,10 +34,23 @@ def _op(module, indices, offsets, psw):
     return module(indices, offsets, psw)
 
 
-def _check_module(oracle, module, indices, offsets, psw, label, b_sel=None):
-    """Run the op on the GPU and compare with the oracle on the (sub)problem."""
-    _say(f"[gpu] {label}: T={len(module.specs)} N={indices.numel()} bags={offsets.numel() - 1}")
-    out = _op(module, indices, offsets, psw)
+def _capi_run(pkg, module, indices, offsets, psw, flags):
+    """The forward through the C ABI with TBE_FLAG_* switches (same inputs as the op)."""
+    return pkg.capi.forward_tensors(module.weights_dev, module.weights_offsets, module.weights_tys, module.D_offsets,
+                                    indices, offsets, int(module.pooling_mode), psw, module.output_dtype,
+                                    module.row_alignment, getattr(module, "fp8_exponent_bits", -1),
+                                    getattr(module, "fp8_exponent_bias", -1), flags=flags)
+
+
+def _check_module(oracle, module, indices, offsets, psw, label, b_sel=None, flags=None):
+    """Run the op on the GPU (through the C ABI with `flags` when given) and compare
+    with the oracle on the (sub)problem."""
+    import fbgemm_ascend_amd as pkg
+    _say(f"[gpu] {label}: T={len(module.specs)} N={indices.numel()} bags={offsets.numel() - 1} flags={flags}")
+    if flags is None:
+        out = _op(module, indices, offsets, psw)
+    else:
+        out = _capi_run(pkg, module, indices, offsets, psw if int(module.pooling_mode) != 2 else None, flags)
     torch.cuda.synchronize()
     pm = int(module.pooling_mode)
     prob = compact_problem(module, indices, offsets, psw if pm != 2 else None, b_sel)
@@ -176,20 +189,25 @@ def _matrix_params(types):
     return params
 
 
+@pytest.mark.parametrize("kernel", ["default", "stream"])
 @pytest.mark.parametrize("T", list(range(1, 11)))
 @pytest.mark.parametrize("ty,pm,weighted,idx_dtype,out_ty", _matrix_params([FP8]))
-def test_random_multi_table_forward_fp8(pkg, oracle, gpu, T, ty, pm, weighted, idx_dtype, out_ty):
+def test_random_multi_table_forward_fp8(pkg, oracle, gpu, T, ty, pm, weighted, idx_dtype, out_ty, kernel):
     seed = zlib.crc32(repr((T, ty, pm, weighted, str(idx_dtype), out_ty)).encode()) & 0xFFFF
     m, idx, off, psw = _random_case(pkg, gpu, seed, T, ty, pm, weighted, idx_dtype, out_ty)
-    _check_module(oracle, m, idx, off, psw, f"fp8 T={T} pm={pm} w={weighted} {idx_dtype} out={out_ty}")
+    flags = pkg.capi.TBE_FLAG_FORCE_STREAM if kernel == "stream" else None
+    _check_module(oracle, m, idx, off, psw, f"fp8 T={T} pm={pm} w={weighted} {idx_dtype} out={out_ty}", flags=flags)
 
 
+@pytest.mark.parametrize("kernel", ["default", "stream"])
 @pytest.mark.parametrize("T", [2, 5])
 @pytest.mark.parametrize("ty,pm,weighted,idx_dtype,out_ty", _matrix_params([INT8, INT4, INT2, FP16, FP32, BF16]))
-def test_random_multi_table_forward_types(pkg, oracle, gpu, T, ty, pm, weighted, idx_dtype, out_ty):
+def test_random_multi_table_forward_types(pkg, oracle, gpu, T, ty, pm, weighted, idx_dtype, out_ty, kernel):
     seed = zlib.crc32(repr((T, ty, pm, weighted, str(idx_dtype), out_ty, "t")).encode()) & 0xFFFF
     m, idx, off, psw = _random_case(pkg, gpu, seed, T, ty, pm, weighted, idx_dtype, out_ty)
-    _check_module(oracle, m, idx, off, psw, f"ty={ty} T={T} pm={pm} w={weighted} {idx_dtype} out={out_ty}")
+    flags = pkg.capi.TBE_FLAG_FORCE_STREAM if kernel == "stream" else None
+    _check_module(oracle, m, idx, off, psw, f"ty={ty} T={T} pm={pm} w={weighted} {idx_dtype} out={out_ty}",
+                  flags=flags)
 
 
 BAG_TABLES = [[(1000, 16), (2000, 16)], [(2000, 256), (1000, 256)], [(2000, 512), (1000, 512)],
@@ -334,6 +352,65 @@ def test_config_full_parity(pkg, oracle, gpu, cid):
     _say(f"[gpu] config {cid}: max err/limit = {ratio:.3f}")
     del wl
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("cid", [0, 1, 2, 3])
+@pytest.mark.parametrize("kernel", ["per_bag", "stream"])
+def test_config_kernel_choice_parity(pkg, oracle, gpu, cid, kernel):
+    """Both pooled kernels meet the same bar whatever the default choice for the
+    group: TBE_FLAG_NO_STREAM forces the per-bag kernel, TBE_FLAG_FORCE_STREAM the
+    row-stream kernel for every eligible group (configs at 1/8 batch)."""
+    from fbgemm_ascend_amd.workloads import make_workload
+    wl = make_workload(cid, device=gpu, batch=max(1, {0: 512, 1: 2048, 2: 8192, 3: 16384}[cid] // 8))
+    m = wl.module
+    flags = pkg.capi.TBE_FLAG_NO_STREAM if kernel == "per_bag" else pkg.capi.TBE_FLAG_FORCE_STREAM
+    _say(f"[gpu] {kernel} kernel, config {cid}")
+    out = pkg.capi.forward_tensors(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets, wl.indices,
+                                   wl.offsets, int(m.pooling_mode), wl.per_sample_weights, m.output_dtype,
+                                   flags=flags)
+    torch.cuda.synchronize()
+    prob = compact_problem(m, wl.indices, wl.offsets, wl.per_sample_weights, None)
+    _, ref32 = run_oracle(oracle, prob, int(m.pooling_mode), m.output_dtype, m.row_alignment)
+    assert_bag_parity(out, prob, ref32, int(m.pooling_mode), m.output_dtype, f"{kernel} config {cid}")
+    del wl
+    torch.cuda.empty_cache()
+
+
+def test_double_table_forward_bag_stream(pkg, oracle, gpu):
+    """The reference's fixed two-table bag lists (T:418-425) through the row-stream
+    kernel, every output dtype, weighted MEAN and plain SUM."""
+    for tables in BAG_TABLES:
+        for out_ty in (FP16, FP32, BF16):
+            for pm, weighted in ((0, False), (1, True)):
+                m, idx, off, psw = _random_case(pkg, gpu, 1234, 2, FP8, pm, weighted, torch.int64, out_ty,
+                                                tables=tables, L_list=[40, 50])
+                _check_module(oracle, m, idx, off, psw, f"double bag {tables} pm={pm} out={out_ty}",
+                              flags=pkg.capi.TBE_FLAG_FORCE_STREAM)
+
+
+def test_stream_kernel_bag_splits(pkg, oracle, gpu):
+    """Row-stream kernel: one very long bag among short and empty ones (slots that get
+    no bag, a bag that spans several index chunks, empty bags at a wave's start and
+    end), every bags-per-wave boundary position (B = 1..70)."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    specs = [(300, 128, SparseType.INT4), (200, 128, SparseType.INT8), (100, 256, SparseType.FP16)]
+    rnd = random.Random(7)
+    for B in (1, 2, 31, 32, 33, 63, 64, 65, 70):
+        for pm, weighted in ((0, False), (1, True)):
+            m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device=gpu, pooling_mode=pm, output_dtype=FP32)
+            m.fill_random_weights(B)
+            lens = [rnd.choice([0, 0, 1, 3, 17, 40]) for _ in range(3 * B)]
+            lens[0] = 0
+            lens[-1] = 0
+            lens[rnd.randrange(1, 3 * B - 1)] = 700
+            off = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int64, device=gpu)
+            N = int(off[-1])
+            g = torch.Generator(device=gpu)
+            g.manual_seed(B)
+            idx = torch.randint(-3, 320, (N,), device=gpu, generator=g)
+            psw = torch.rand(N, device=gpu, generator=g) if weighted else None
+            _check_module(oracle, m, idx, off, psw, f"stream splits B={B} pm={pm}",
+                          flags=pkg.capi.TBE_FLAG_FORCE_STREAM)
 
 
 def test_config4_sampled_parity(pkg, oracle, gpu):

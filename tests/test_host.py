@@ -37,7 +37,7 @@ def test_abi_version_and_struct_layout(pkg, tmp_path):
     """The ctypes mirror has the C compiler's sizes and field offsets for every struct."""
     import subprocess
     c = pkg.capi
-    assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 2
+    assert c.lib().tbe_nbit_abi_version() == c.ABI_VERSION == 3
     structs = [c.TbeTableDesc, c.TbePlanInput, c.TbePlanGroup, c.TbePlanSummary, c.TbeNbitArgs,
                c.TbePermutePooledArgs, c.TbeBlockBucketizeArgs]
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tbe_nbit.h"', '#include "tbe_pooled_ops.h"',
