@@ -39,8 +39,9 @@ def _parse():
     ap.add_argument("--flags", type=int, default=0, help="TBE_FLAG_* tuning switches (C-ABI path)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB device copy instead (calibrates rocprof FETCH/WRITE_SIZE)")
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "tbe_int4_cfg2_traffic.json"),
-                    help="HBM traffic per launch measured with rocprofv3 --pmc (JSON)")
+    ap.add_argument("--traffic", default=None,
+                    help="HBM traffic per launch measured with rocprofv3 --pmc (JSON); default: "
+                         "profiles/tbe_cfg<config>_traffic.json when it exists")
     ap.add_argument("--op", default="tbe", choices=["tbe", "permute_pooled_embs", "block_bucketize_sparse_features"],
                     help="tbe: the headline TBE forward; permute_pooled_embs: the pooled-output "
                          "permutation on config 4's output shape; block_bucketize_sparse_features: the "
@@ -291,8 +292,9 @@ def main():
     alg_bytes = wl.algorithmic_bytes()
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     traffic = None
-    if os.path.exists(args.traffic):
-        with open(args.traffic) as f:
+    tpath = args.traffic or os.path.join(ROOT, "profiles", f"tbe_cfg{args.config}_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
             t = json.load(f)
         if t.get("config") == args.config:
             traffic = t.get("hbm_bytes_per_launch")
