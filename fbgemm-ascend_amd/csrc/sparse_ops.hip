@@ -8,12 +8,12 @@
 // Three phases, as in BA:142-231: count the indices of every (bucket, row)
 // segment, turn the counts into segment offsets with a device scan, scatter.  One
 // 64-wide wavefront owns one row at a time and walks its indices 64 per step.
-// Lanes that map to the same bucket are grouped with a ballot loop (one pass per
-// distinct bucket in the step); a lane's rank is the group's base plus the number
-// of lower lanes in its group.  For my_size <= 64 the row's per-bucket counters
-// and write cursors live in one VGPR (lane b = bucket b), read with v_readlane, so
-// the loop touches no memory; larger my_size keeps them in memory and advances
-// them with one atomic per group.  Only the owning wave touches a row's counters,
+// For my_size <= 64 the row's per-bucket counters and write cursors live in one
+// VGPR (lane b = bucket b) and a lane's rank among the lower lanes of its bucket
+// comes from one ballot per bit of the bucket number (no pass per bucket, no
+// memory); larger my_size groups the lanes of a bucket with a ballot loop (one
+// pass per distinct bucket in the step) and advances in-memory counters with one
+// atomic per group.  Only the owning wave touches a row's counters,
 // so segments are filled in row order and the result is deterministic, including
 // for sequence = 0 where the reference's per-lane atomics (BK:582-584) leave the
 // order inside a segment unspecified.
@@ -59,6 +59,7 @@ struct BBParams {
   int64_t B;                    // rows per feature without batch_size_offsets
   int32_t F;
   int32_t keep;
+  int32_t bucket_bits;          // ceil(log2(my_size)) when my_size <= 64
 };
 
 __device__ __forceinline__ int64_t uni(int64_t v) {
@@ -131,6 +132,21 @@ __device__ __forceinline__ RowCtx<IT> row_ctx(const BBParams<IT, OT>& p, int64_t
   return c;
 }
 
+// a / d and a % d; 64-bit operands that fit in 32 bits take the 32-bit divide.
+template <typename UIT>
+__device__ __forceinline__ void divmod(UIT a, UIT d, UIT& q, UIT& r) {
+  if constexpr (sizeof(UIT) == 8) {
+    if (((a | d) >> 32) == 0) {
+      const uint32_t q32 = static_cast<uint32_t>(a) / static_cast<uint32_t>(d);
+      q = q32;
+      r = a - static_cast<UIT>(q32) * d;
+      return;
+    }
+  }
+  q = a / d;
+  r = a - q * d;
+}
+
 // BK:423-453 (bucket) and BK:560-603 (new index).  Returns false for an index
 // whose bucket falls outside [0, my_size).
 template <typename IT>
@@ -153,11 +169,16 @@ __device__ __forceinline__ bool map_index(const RowCtx<IT>& c, std::make_unsigne
     else if (in) nidx = static_cast<IT>(static_cast<UIT>(u - static_cast<UIT>(c.pos[lb])));
     else nidx = static_cast<IT>(static_cast<uint64_t>(u) / my);
   } else if (c.blk != 0 && u < c.gsize) {
-    bucket = static_cast<int64_t>(u / c.lsize);
-    nidx = keep ? static_cast<IT>(u) : static_cast<IT>(u % c.lsize);
+    UIT q, r;
+    divmod<UIT>(u, c.lsize, q, r);
+    bucket = static_cast<int64_t>(q);
+    nidx = keep ? static_cast<IT>(u) : static_cast<IT>(r);
   } else {
-    bucket = static_cast<int64_t>((u % c.gb) / c.lbk);
-    nidx = keep ? static_cast<IT>(u) : static_cast<IT>(u / c.gb);
+    UIT q, r, qb, rb;
+    divmod<UIT>(u, c.gb, q, r);
+    divmod<UIT>(r, c.lbk, qb, rb);
+    bucket = static_cast<int64_t>(qb);
+    nidx = keep ? static_cast<IT>(u) : static_cast<IT>(q);
   }
   return static_cast<uint64_t>(bucket) < my;
 }
@@ -172,6 +193,33 @@ __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x &
 
 __device__ __forceinline__ uint64_t lanes_below() {
   return (uint64_t(1) << lane_id()) - 1;  // lane 0: 0
+}
+
+// Bucket ranks without a pass per bucket (my_size <= 64): one ballot per bit of
+// the bucket number; the lanes whose bucket equals `key` are the valid lanes that
+// agree with `key` on every bit.
+constexpr int kMaxBucketBits = 6;
+
+struct BucketBits {
+  uint64_t valid;
+  uint64_t bit[kMaxBucketBits];
+};
+
+__device__ __forceinline__ BucketBits bucket_bits(bool valid, uint32_t bucket, int nbits) {
+  BucketBits r;
+  r.valid = __builtin_amdgcn_ballot_w64(valid);
+#pragma unroll
+  for (int j = 0; j < kMaxBucketBits; ++j)
+    r.bit[j] = j < nbits ? __builtin_amdgcn_ballot_w64(valid && ((bucket >> j) & 1u)) : 0;
+  return r;
+}
+
+__device__ __forceinline__ uint64_t lanes_with_bucket(const BucketBits& bb, uint32_t key, int nbits) {
+  uint64_t m = bb.valid;
+#pragma unroll
+  for (int j = 0; j < kMaxBucketBits; ++j)
+    if (j < nbits) m &= ((key >> j) & 1u) ? bb.bit[j] : ~bb.bit[j];
+  return m;
 }
 
 template <typename T>
@@ -200,6 +248,12 @@ __global__ __launch_bounds__(kBBBlock) void bb_count(BBParams<IT, OT> p) {
         int64_t b = 0;
         IT v;
         bool valid = i < c.e && map_index<IT>(c, static_cast<UIT>(p.indices[i]), p.my_size, p.keep, b, v);
+        if constexpr (REG) {
+          // lane l counts the indices of bucket l
+          const BucketBits bb = bucket_bits(valid, static_cast<uint32_t>(b), p.bucket_bits);
+          cnt += static_cast<uint32_t>(__builtin_popcountll(lanes_with_bucket(bb, lane_id(), p.bucket_bits)));
+          continue;
+        }
         uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
         while (pending) {
           const int leader = __builtin_ctzll(pending);
@@ -207,11 +261,7 @@ __global__ __launch_bounds__(kBBBlock) void bb_count(BBParams<IT, OT> p) {
           const bool mine = valid && b == bl;
           const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
           const uint32_t k = static_cast<uint32_t>(__builtin_popcountll(m));
-          if constexpr (REG) {
-            if (lane_id() == bl) cnt += k;
-          } else {
-            if (lane_id() == leader) add_count(p.new_lengths + bl * p.L + r, k);
-          }
+          if (lane_id() == leader) add_count(p.new_lengths + bl * p.L + r, k);
           pending &= ~m;
           valid = valid && !mine;
         }
@@ -245,26 +295,32 @@ __global__ __launch_bounds__(kBBBlock) void bb_scatter(BBParams<IT, OT> p) {
       IT v = 0;
       const bool valid0 = i < c.e && map_index<IT>(c, static_cast<UIT>(p.indices[i]), p.my_size, p.keep, b, v);
       bool valid = valid0;
-      uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
       int64_t w = 0;
+      uint64_t pending = 0;
+      if constexpr (REG) {
+        // rank among the lower lanes of the same bucket, after the bucket's cursor
+        // (lane b holds it); lane l then advances bucket l's cursor
+        const BucketBits bb = bucket_bits(valid0, static_cast<uint32_t>(b), p.bucket_bits);
+        const uint64_t mine = lanes_with_bucket(bb, static_cast<uint32_t>(b), p.bucket_bits);
+        const int src = static_cast<int>(b & 63) * 4;
+        const int64_t seg0 = static_cast<int64_t>(
+            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(cur >> 32)))) << 32) |
+            static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(cur & 0xFFFFFFFF))));
+        w = seg0 + __builtin_popcountll(mine & lanes_below());
+        cur += __builtin_popcountll(lanes_with_bucket(bb, lane_id(), p.bucket_bits));
+      } else {
+        pending = __builtin_amdgcn_ballot_w64(valid);
+      }
       while (pending) {
         const int leader = __builtin_ctzll(pending);
         const int64_t bl = uni(__builtin_amdgcn_readlane(static_cast<int>(b), leader)) & 0xFFFFFFFFll;
         const bool mine = valid && b == bl;
         const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
         const uint32_t k = static_cast<uint32_t>(__builtin_popcountll(m));
-        int64_t seg0;
-        if constexpr (REG) {
-          seg0 = static_cast<int64_t>(
-              (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cur >> 32), static_cast<int>(bl)))) << 32) |
-              static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cur & 0xFFFFFFFF), static_cast<int>(bl))));
-          if (lane_id() == bl) cur += k;
-        } else {
-          uint32_t old = 0;
-          if (lane_id() == leader) old = atomicAdd(p.done + bl * p.L + r, k);
-          old = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(old), leader));
-          seg0 = static_cast<int64_t>(p.new_offsets[bl * p.L + r]) + old;
-        }
+        uint32_t old = 0;
+        if (lane_id() == leader) old = atomicAdd(p.done + bl * p.L + r, k);
+        old = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(old), leader));
+        const int64_t seg0 = static_cast<int64_t>(p.new_offsets[bl * p.L + r]) + old;
         if (mine) w = seg0 + __builtin_popcountll(m & lanes_below());
         pending &= ~m;
         valid = valid && !mine;
@@ -391,6 +447,8 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s) {
   p.B = a->batch_size_offsets ? 0 : a->lengths_size / a->num_features;
   p.F = a->num_features;
   p.keep = a->keep_orig_idx;
+  p.bucket_bits = 0;
+  while (p.bucket_bits < kMaxBucketBits && (int64_t(1) << p.bucket_bits) < a->my_size) ++p.bucket_bits;
   const int64_t nseg = a->my_size * a->lengths_size;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
