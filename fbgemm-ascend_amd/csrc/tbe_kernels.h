@@ -70,8 +70,9 @@ constexpr int kUnrollWide = 8;
 // Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle).
 constexpr int kRsrcWord3 = 0x00020000;
 // Offset that fails the buffer range check, so the load returns zero (rows past
-// the bag, rejected indices).  Row offsets of 32-bit tables stay below 2^31.
-constexpr uint32_t kNoRow = 0x80000000u;
+// the bag, rejected indices).  32-bit tables span at most kNoRow bytes, and a
+// lane's column offset stays below 64 KiB, so kNoRow + column never wraps.
+constexpr uint32_t kNoRow = 0xFFFE0000u;
 
 // Unsigned division by a runtime-invariant divisor with one multiply-high
 // (Granlund & Montgomery, PLDI 1994): q = (mulhi(n, mul) + n) >> shift,
@@ -888,7 +889,7 @@ __device__ __forceinline__ void finish_bag_fast(const KParams& p, const StagedBa
 
 // ---------------------------------------------------------------- pooled bag, 64-bit tables
 
-// Same contract for tables whose rows span 2 GiB or more: 64-bit addresses and
+// Same contract for tables whose rows span more than kNoRow bytes: 64-bit addresses and
 // explicit masks instead of the buffer range check.  Lanes per row are a runtime
 // value here.
 template <int WT, bool WEIGHTED>

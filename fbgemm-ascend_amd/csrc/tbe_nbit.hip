@@ -316,7 +316,7 @@ int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_or
     auto it = std::upper_bound(starts.begin(), starts.end(), descs[t].weights_offset);
     const int64_t end = it == starts.end() ? in->dev_weights_bytes : *it;
     descs[t].num_rows = (end - descs[t].weights_offset) / descs[t].row_stride;
-    if (descs[t].num_rows * descs[t].row_stride <= 0x7FFFFFFFLL) descs[t].flags |= TBE_TABLE_OFFSET32;
+    if (descs[t].num_rows * descs[t].row_stride <= static_cast<int64_t>(kNoRow)) descs[t].flags |= TBE_TABLE_OFFSET32;
     // row-stream kernel: at least 4 lanes per slot, whole lane loads
     const int vw = stream_vw_of(descs[t].weight_ty, descs[t].log2_lanes);
     if ((descs[t].flags & TBE_TABLE_OFFSET32) && (1 << descs[t].log2_lanes) >= 4 * vw &&

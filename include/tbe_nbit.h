@@ -72,8 +72,9 @@ typedef struct TbeTableDesc {
   uint8_t flags;          /* TBE_TABLE_* bits, set by the planner                 */
 } TbeTableDesc;
 
-/* TbeTableDesc.flags: the table's rows span < 2 GiB, so the kernels address them
- * with 32-bit offsets from the table base (buffer loads with range checking). */
+/* TbeTableDesc.flags: the table's rows span at most 0xFFFE0000 bytes (4 GiB less
+ * 128 KiB), so the kernels address them with 32-bit offsets from the table base
+ * (buffer loads with range checking). */
 #define TBE_TABLE_OFFSET32 0x1
 /* TbeTableDesc.flags: OFFSET32 and a payload of at least 8 words in an even
  * number of words, so the table is gathered by the row-stream kernel (8-byte

@@ -388,6 +388,31 @@ def test_double_table_forward_bag_stream(pkg, oracle, gpu):
                               flags=pkg.capi.TBE_FLAG_FORCE_STREAM)
 
 
+@pytest.mark.parametrize("kernel", ["per_bag", "stream"])
+def test_table_above_2gib_32bit_addressing(pkg, oracle, gpu, kernel):
+    """A 2.3 GB FP16 table (rows beyond the 2 GiB byte offset) next to a small INT4
+    table, addressed with 32-bit offsets; indices hit the table's last rows."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    if _free_gib() < 8:
+        pytest.skip("needs ~3 GiB of free HBM")
+    rows = 4_500_000
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(rows, 256, SparseType.FP16), (1000, 128, SparseType.INT4)],
+                                                device=gpu, pooling_mode=0, output_dtype=FP32)
+    m.fill_random_weights(11)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(11)
+    B, L = 64, 24
+    off = torch.arange(0, 2 * B * L + 1, L, dtype=torch.int64, device=gpu)
+    big = torch.randint(rows - 20000, rows + 3, (B * L,), device=gpu, generator=g)  # last rows, a few out of range
+    big[::7] = torch.randint(0, rows, (big[::7].numel(),), device=gpu, generator=g)
+    small = torch.randint(0, 1000, (B * L,), device=gpu, generator=g)
+    idx = torch.cat([big, small])
+    flags = pkg.capi.TBE_FLAG_NO_STREAM if kernel == "per_bag" else pkg.capi.TBE_FLAG_FORCE_STREAM
+    _check_module(oracle, m, idx, off, None, f"2.3 GB table, {kernel}", flags=flags)
+    del m
+    torch.cuda.empty_cache()
+
+
 def test_stream_kernel_bag_splits(pkg, oracle, gpu):
     """Row-stream kernel: one very long bag among short and empty ones (slots that get
     no bag, a bag that spans several index chunks, empty bags at a wave's start and

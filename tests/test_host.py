@@ -113,6 +113,19 @@ def test_plan_groups_tables_by_kernel_shape(pkg):
     assert sorted(order.tolist()) == list(range(6))
 
 
+def test_plan_offset32_covers_tables_below_4gib(pkg):
+    """32-bit table addressing (and with it the per-bag and row-stream kernels) holds
+    up to 0xFFFE0000 bytes of rows; beyond that the 64-bit kernel takes the table."""
+    limit = 0xFFFE0000
+    for nbytes in (2 ** 31 + 4096, limit, limit + 80 * 2000):
+        descs, order, s = pkg.capi.plan([0], [INT4], [0, 128], nbytes)
+        rows = nbytes // 80
+        o32 = bool(descs[0].flags & pkg.capi.TBE_TABLE_OFFSET32)
+        assert descs[0].num_rows == rows
+        assert o32 == (rows * 80 <= limit), nbytes
+        assert s.groups[0].offset32 == int(o32)
+
+
 @pytest.mark.parametrize("kw,match", [
     (dict(tys=[9]), "unsupported weight type"),
     (dict(tys=[INT4], dofs=[0, 12]), "4-byte words"),
