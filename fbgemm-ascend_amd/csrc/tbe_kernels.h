@@ -345,6 +345,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+typedef uint32_t tbe_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t tbe_u32x4 __attribute__((ext_vector_type(4)));
+
+// Output stores: the output is written once and never read back here, so it is
+// stored non-temporally and does not evict from L2 the embedding rows that bags
+// share (config 2: 123 -> 121 us, config 3: 876 -> 857 us).  Index chunks keep
+// plain loads: consecutive chunks share cache lines.
+template <typename T>
+__device__ __forceinline__ void out_store(T* p, T v) {
+  __builtin_nontemporal_store(v, p);
+}
+
 template <int E>
 __device__ __forceinline__ void store_f32(float* o, const float (&r)[E]) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(o);
@@ -352,19 +364,21 @@ __device__ __forceinline__ void store_f32(float* o, const float (&r)[E]) {
     if ((a & 15u) == 0) {
 #pragma unroll
       for (int i = 0; i < E; i += 4)
-        *reinterpret_cast<float4*>(o + i) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
+        out_store(reinterpret_cast<tbe_u32x4*>(o + i), tbe_u32x4{__float_as_uint(r[i]), __float_as_uint(r[i + 1]),
+                                                             __float_as_uint(r[i + 2]), __float_as_uint(r[i + 3])});
       return;
     }
   }
   if constexpr (E % 2 == 0) {
     if ((a & 7u) == 0) {
 #pragma unroll
-      for (int i = 0; i < E; i += 2) *reinterpret_cast<float2*>(o + i) = make_float2(r[i], r[i + 1]);
+      for (int i = 0; i < E; i += 2)
+        out_store(reinterpret_cast<tbe_u32x2*>(o + i), tbe_u32x2{__float_as_uint(r[i]), __float_as_uint(r[i + 1])});
       return;
     }
   }
 #pragma unroll
-  for (int i = 0; i < E; ++i) o[i] = r[i];
+  for (int i = 0; i < E; ++i) out_store(o + i, r[i]);
 }
 
 template <int E>
@@ -374,12 +388,9 @@ __device__ __forceinline__ void store_b16(uint16_t* o, const uint16_t (&b)[E]) {
     if ((a & 15u) == 0) {
 #pragma unroll
       for (int i = 0; i < E; i += 8) {
-        uint4 w;
-        w.x = b[i] | (uint32_t(b[i + 1]) << 16);
-        w.y = b[i + 2] | (uint32_t(b[i + 3]) << 16);
-        w.z = b[i + 4] | (uint32_t(b[i + 5]) << 16);
-        w.w = b[i + 6] | (uint32_t(b[i + 7]) << 16);
-        *reinterpret_cast<uint4*>(o + i) = w;
+        const tbe_u32x4 w{b[i] | (uint32_t(b[i + 1]) << 16), b[i + 2] | (uint32_t(b[i + 3]) << 16),
+                          b[i + 4] | (uint32_t(b[i + 5]) << 16), b[i + 6] | (uint32_t(b[i + 7]) << 16)};
+        out_store(reinterpret_cast<tbe_u32x4*>(o + i), w);
       }
       return;
     }
@@ -388,10 +399,8 @@ __device__ __forceinline__ void store_b16(uint16_t* o, const uint16_t (&b)[E]) {
     if ((a & 7u) == 0) {
 #pragma unroll
       for (int i = 0; i < E; i += 4) {
-        uint2 w;
-        w.x = b[i] | (uint32_t(b[i + 1]) << 16);
-        w.y = b[i + 2] | (uint32_t(b[i + 3]) << 16);
-        *reinterpret_cast<uint2*>(o + i) = w;
+        out_store(reinterpret_cast<tbe_u32x2*>(o + i),
+                  tbe_u32x2{b[i] | (uint32_t(b[i + 1]) << 16), b[i + 2] | (uint32_t(b[i + 3]) << 16)});
       }
       return;
     }
@@ -400,12 +409,12 @@ __device__ __forceinline__ void store_b16(uint16_t* o, const uint16_t (&b)[E]) {
     if ((a & 3u) == 0) {
 #pragma unroll
       for (int i = 0; i < E; i += 2)
-        *reinterpret_cast<uint32_t*>(o + i) = b[i] | (uint32_t(b[i + 1]) << 16);
+        out_store(reinterpret_cast<uint32_t*>(o + i), b[i] | (uint32_t(b[i + 1]) << 16));
       return;
     }
   }
 #pragma unroll
-  for (int i = 0; i < E; ++i) o[i] = b[i];
+  for (int i = 0; i < E; ++i) out_store(o + i, b[i]);
 }
 
 // Write E consecutive output elements starting at element `pos` of the output,
@@ -435,12 +444,14 @@ __device__ __forceinline__ void store_slice(const KParams& p, int64_t pos, const
     float* o = static_cast<float*>(p.out) + pos;
     if (vec && E % 4 == 0) {
 #pragma unroll
-      for (int i = 0; i < E; i += 4) *reinterpret_cast<float4*>(o + i) = make_float4(r[i], r[i + 1], r[i + 2], r[i + 3]);
+      for (int i = 0; i < E; i += 4)
+        out_store(reinterpret_cast<tbe_u32x4*>(o + i), tbe_u32x4{__float_as_uint(r[i]), __float_as_uint(r[i + 1]),
+                                                             __float_as_uint(r[i + 2]), __float_as_uint(r[i + 3])});
     } else if (vec && E == 2) {
-      *reinterpret_cast<float2*>(o) = make_float2(r[0], r[1]);
+      out_store(reinterpret_cast<tbe_u32x2*>(o), tbe_u32x2{__float_as_uint(r[0]), __float_as_uint(r[1])});
     } else {
 #pragma unroll
-      for (int i = 0; i < E; ++i) o[i] = r[i];
+      for (int i = 0; i < E; ++i) out_store(o + i, r[i]);
     }
     return;
   }
@@ -456,7 +467,7 @@ __device__ __forceinline__ void store_slice(const KParams& p, int64_t pos, const
   if constexpr (E >= 2) {
     if (!vec) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) o[i] = b[i];
+      for (int i = 0; i < E; ++i) out_store(o + i, b[i]);
       return;
     }
     uint32_t w[E / 2];
@@ -464,15 +475,16 @@ __device__ __forceinline__ void store_slice(const KParams& p, int64_t pos, const
     for (int i = 0; i < E / 2; ++i) w[i] = b[2 * i] | (uint32_t(b[2 * i + 1]) << 16);
     if constexpr (E % 8 == 0) {
 #pragma unroll
-      for (int i = 0; i < E / 2; i += 4) *reinterpret_cast<uint4*>(o + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      for (int i = 0; i < E / 2; i += 4)
+        out_store(reinterpret_cast<tbe_u32x4*>(o + 2 * i), tbe_u32x4{w[i], w[i + 1], w[i + 2], w[i + 3]});
     } else if constexpr (E == 4) {
-      *reinterpret_cast<uint2*>(o) = make_uint2(w[0], w[1]);
+      out_store(reinterpret_cast<tbe_u32x2*>(o), tbe_u32x2{w[0], w[1]});
     } else {
-      *reinterpret_cast<uint32_t*>(o) = w[0];
+      out_store(reinterpret_cast<uint32_t*>(o), w[0]);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < E; ++i) o[i] = b[i];
+    for (int i = 0; i < E; ++i) out_store(o + i, b[i]);
   }
 }
 
@@ -1062,6 +1074,7 @@ __device__ __forceinline__ void load_stream_chunk(const KParams& p, uint32_t q0,
   idx = -1;
   w = 0.f;
   if (q < end) {
+    // plain loads: a slot's consecutive chunks share cache lines
     idx = static_cast<const IndexT*>(p.indices)[q];
     if constexpr (WEIGHTED) w = p.psw[q];
   }
