@@ -42,8 +42,10 @@ def _parse():
     ap.add_argument("--traffic", default=None,
                     help="HBM traffic per launch measured with rocprofv3 --pmc (JSON); default: "
                          "profiles/tbe_cfg<config>_traffic.json when it exists")
-    ap.add_argument("--op", default="tbe", choices=["tbe", "permute_pooled_embs", "block_bucketize_sparse_features"],
-                    help="tbe: the headline TBE forward; permute_pooled_embs: the pooled-output "
+    ap.add_argument("--op", default="tbe",
+                    choices=["tbe", "tbe_nobag", "permute_pooled_embs", "block_bucketize_sparse_features"],
+                    help="tbe: the headline TBE forward; tbe_nobag: the same op with pooling_mode NONE on "
+                         "config 2's tables and indices; permute_pooled_embs: the pooled-output "
                          "permutation on config 4's output shape; block_bucketize_sparse_features: the "
                          "reference's stress case (16 features x 8192 samples, 128-512 indices, my_size 16)")
     return ap.parse_args()
@@ -105,6 +107,56 @@ def bench_permute(args, pkg, dev):
                         "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
            "kernel_ms": mean_ms, "kernel_ms_median": ms[len(ms) // 2], "bytes_per_step": nbytes,
            "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
+
+
+def bench_nobag(args, pkg, dev):
+    """pooling_mode NONE (row a9 of the scope, N:44-340) on config 2's tables and
+    indices: every lookup writes its dequantised row, out [N, 128] fp16.  Priced as
+    N x (68 B row + 4 B index + 256 B output)."""
+    import torch
+    from fbgemm_ascend_amd.workloads import make_workload
+
+    wl = make_workload(2, device=dev)
+    m = wl.module
+    op = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function
+
+    def step():
+        return op(dev_weights=m.weights_dev, uvm_weights=m.weights_uvm, weights_placements=m.weights_placements,
+                  weights_offsets=m.weights_offsets, weights_tys=m.weights_tys, D_offsets=m.D_offsets,
+                  total_D=m.total_D, max_int2_D=m.max_int2_D, max_int4_D=m.max_int4_D, max_int8_D=m.max_int8_D,
+                  max_float16_D=m.max_float16_D, max_float32_D=m.max_float32_D, indices=wl.indices,
+                  offsets=wl.offsets, pooling_mode=2, indice_weights=None, output_dtype=m.output_dtype,
+                  lxu_cache_weights=None, lxu_cache_locations=None, row_alignment=m.row_alignment,
+                  max_float8_D=m.max_float8_D, fp8_exponent_bits=m.fp8_exponent_bits,
+                  fp8_exponent_bias=m.fp8_exponent_bias)
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    mean_ms = sum(ms) / len(ms)
+    N = wl.num_indices
+    nbytes = N * (68 + wl.indices.element_size() + 128 * 2)
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    out = {"metric": "TBE nobag lookups/s, 1 GPU", "value": N / (mean_ms * 1e-3), "unit": "lookups/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int4",
+           "data": "synthetic (seeded, generated on device)",
+           "config": {"workload": "config 2 tables and indices, pooling_mode NONE", "lookups": N, "D": 128,
+                      "output": "fp16"},
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+           "kernel_ms": mean_ms, "kernel_ms_median": ms[len(ms) // 2], "bytes_per_step": nbytes,
+           "cpu_baseline": None}
     print(json.dumps(out), flush=True)
 
 
@@ -226,6 +278,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.op == "tbe_nobag":
+        bench_nobag(args, pkg, dev)
+        return
     if args.op == "permute_pooled_embs":
         bench_permute(args, pkg, dev)
         return

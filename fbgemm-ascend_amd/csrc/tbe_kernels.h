@@ -1271,6 +1271,105 @@ __global__ __launch_bounds__(kBlock) void pooled_stream_kernel(KParams p) {
   if (nchunks > 0) chunk_step(std::false_type{});
 }
 
+// ---------------------------------------------------------------- nobag, 32-bit tables
+
+// pooling_mode NONE (N:224-300): output row i is the dequantised row of
+// indices[i].  One wave takes 64 consecutive positions; per table segment the 64
+// indices arrive with one coalesced load, their row offsets reach the row lanes
+// by ds_bpermute, and every row load of the segment is issued before the first
+// is decoded.  Specialised per (weight type, lanes per row) like the pooled
+// kernels; segments of other tables are left to their own group's launch.
+
+// Decoded (exact) values of one payload word, INT4 through byte conversions.
+template <int WT>
+__device__ __forceinline__ void decode_word(uint32_t d, float (&v)[Traits<WT>::kEpd], const Fp8Consts& c) {
+  if constexpr (WT == TBE_TY_INT4) {
+    const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = static_cast<float>((lo >> (8 * k)) & 0xFFu);
+      v[2 * k + 1] = static_cast<float>((hi >> (8 * k)) & 0xFFu);
+    }
+  } else {
+    decode<WT>(d, v, c);
+  }
+}
+
+template <int WT, int LG, typename IndexT>
+__device__ __forceinline__ void nobag_segment(const KParams& p, const TbeTableDesc& td, int64_t a, int n) {
+  constexpr int E = Traits<WT>::kEpd;
+  constexpr bool HDR = Traits<WT>::kHdr;
+  constexpr int R = kWave >> LG;               // rows per load instruction
+  constexpr int U = kWave / R;                 // load instructions per 64 rows
+  constexpr int UB = U < 16 ? U : 16;          // issued together
+  const int lane = threadIdx.x & (kWave - 1);
+  const int slot = lane >> LG;
+  const uint32_t rows = static_cast<uint32_t>(td.num_rows);
+  const uint32_t stride = static_cast<uint32_t>(td.row_stride);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.weights + td.weights_offset), 0, static_cast<int>(rows * stride), kRsrcWord3);
+  const uint64_t raw = load_index_chunk<IndexT>(p, a, n);
+  const int64_t iv = sizeof(IndexT) == 8 ? static_cast<int64_t>(raw) : static_cast<int64_t>(static_cast<int32_t>(raw));
+  const uint32_t off = (lane < n && iv >= 0 && iv < static_cast<int64_t>(rows)) ? static_cast<uint32_t>(iv) * stride
+                                                                                 : kNoRow;
+  const bool vec = (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0 && p.out_stride % E == 0;
+  for (int ct = 0; ct < td.col_tiles; ++ct) {
+    const int dw = ct * kWave + (lane & ((1 << LG) - 1));
+    const bool col_ok = dw < td.data_dwords;
+    const uint32_t col = static_cast<uint32_t>(td.data_offset + (col_ok ? 4 * dw : 0));
+#pragma unroll
+    for (int u0 = 0; u0 < U; u0 += UB) {
+      if (u0 * R >= n) break;  // wave-uniform
+      uint32_t d[UB], h[UB];
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        const uint32_t o = static_cast<uint32_t>(
+            __builtin_amdgcn_ds_bpermute(((u0 + u) * R + slot) * 4, static_cast<int>(off)));
+        d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o + col), 0, 0));
+        h[u] = HDR ? static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o), 0, 0)) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        const int row = (u0 + u) * R + slot;
+        if (row < n && col_ok) {
+          float v[E], r[E];
+          decode_word<WT>(d[u], v, p.fp8);
+          // a rejected index reads a zero word and header: scale 0, bias 0 -> zeros
+          const float sc = HDR ? h16lo(h[u]) : 1.f, bi = HDR ? h16hi(h[u]) : 0.f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) r[e] = HDR ? fmaf(sc, v[e], bi) : v[e];
+          store_slice<E>(p, (a + row) * p.out_stride + static_cast<int64_t>(dw) * E, r, vec);
+        }
+      }
+    }
+  }
+}
+
+template <int WT, int LG, typename IndexT>
+__global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
+  const int wv = uniform(threadIdx.x >> 6);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wv;
+  if (item >= p.num_items) return;
+  const int64_t i0 = item * kWave;
+  const int64_t i1 = min(i0 + kWave, p.num_indices);
+  // last table whose first index is <= i0 (N:57-78 walks tables by offset_per_key)
+  int lo = 0, hi = p.T - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (load_offset(p, static_cast<int64_t>(mid) * p.B) <= i0) lo = mid; else hi = mid - 1;
+  }
+  for (int t = lo; t < p.T; ++t) {
+    const int64_t tb = load_offset(p, static_cast<int64_t>(t) * p.B);
+    const int64_t te = load_offset(p, static_cast<int64_t>(t + 1) * p.B);
+    if (tb >= i1) break;
+    const int64_t a = max(tb, i0), e = min(te, i1);
+    if (a >= e) continue;
+    const TbeTableDesc td = load_desc(p.tables + t);
+    if (td.weight_ty != WT || td.log2_lanes != LG || !(td.flags & TBE_TABLE_OFFSET32)) continue;
+    nobag_segment<WT, LG, IndexT>(p, td, a, static_cast<int>(e - a));
+  }
+}
+
 // ---------------------------------------------------------------- pooled kernels
 
 
@@ -1370,6 +1469,17 @@ KernelFn stream_kernel_for(bool index64, bool weighted) {
   if (index64)
     return weighted ? pooled_stream_kernel<WT, LG, int64_t, true> : pooled_stream_kernel<WT, LG, int64_t, false>;
   return weighted ? pooled_stream_kernel<WT, LG, int32_t, true> : pooled_stream_kernel<WT, LG, int32_t, false>;
+}
+
+template <int WT>
+KernelFn nobag_kernel_lg(int lg, bool index64) {
+  switch (lg) {
+#define TBE_NOBAG_CASE(L) \
+    case L: return index64 ? nobag_fast_kernel<WT, L, int64_t> : nobag_fast_kernel<WT, L, int32_t>;
+    TBE_NOBAG_CASE(0) TBE_NOBAG_CASE(1) TBE_NOBAG_CASE(2) TBE_NOBAG_CASE(3) TBE_NOBAG_CASE(4) TBE_NOBAG_CASE(5)
+#undef TBE_NOBAG_CASE
+    default: return index64 ? nobag_fast_kernel<WT, 6, int64_t> : nobag_fast_kernel<WT, 6, int32_t>;
+  }
 }
 
 template <int WT>

@@ -18,23 +18,31 @@ namespace tbe {
 // instantiated once, in tbe_kern_<type>.hip
 extern template KernelFn fast_kernel_lg<TBE_TY_FP32>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP32>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_FP32>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_FP16>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP16>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_FP16>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_BF16>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_BF16>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_BF16>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP8>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT8>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT8>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_INT8>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT4>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT4>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_INT4>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT2>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT2>(int, bool, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_INT2>(int, bool);
 
 // ---------------------------------------------------------------- nobag (pooling_mode NONE)
 
 // Rows [i0, i1) of the global index array, all belonging to table td: output row i
-// is the dequantized row of indices[i] (N:224-300).
+// is the dequantized row of indices[i] (N:224-300).  Generic path of tables beyond
+// 32-bit addressing (64-bit addresses, runtime lanes per row).
 template <int WT>
 __device__ __forceinline__ void nobag_rows(const KParams& p, const TbeTableDesc& td, int64_t i0, int64_t i1) {
   constexpr int E = Traits<WT>::kEpd;
@@ -93,6 +101,7 @@ __global__ __launch_bounds__(kBlock) void nobag_kernel(KParams p) {
     const int64_t a = max(tb, i0), e = min(te, i1);
     if (a >= e) continue;
     const TbeTableDesc td = load_desc(p.tables + t);
+    if (td.flags & TBE_TABLE_OFFSET32) continue;  // done by the group's specialised kernel
     switch (td.weight_ty) {
       case TBE_TY_INT4: nobag_rows<TBE_TY_INT4>(p, td, a, e); break;
       case TBE_TY_INT8: nobag_rows<TBE_TY_INT8>(p, td, a, e); break;
@@ -194,6 +203,19 @@ int stream_bags_per_wave(int64_t bags, int64_t resident_waves) {
   const int64_t want = std::max<int64_t>(1, resident_waves) * rounds;
   const int64_t bpw = (bags + want - 1) / want;
   return static_cast<int>(std::min<int64_t>(kMaxBagsPerWave, std::max<int64_t>(4, bpw)));
+}
+
+// Specialised nobag kernel of a 32-bit group.
+KernelFn nobag_kernel_group(const TbePlanGroup& g, bool index64) {
+  switch (g.weight_ty) {
+    case TBE_TY_FP32: return nobag_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64);
+    case TBE_TY_FP16: return nobag_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64);
+    case TBE_TY_BF16: return nobag_kernel_lg<TBE_TY_BF16>(g.log2_lanes, index64);
+    case TBE_TY_FP8:  return nobag_kernel_lg<TBE_TY_FP8>(g.log2_lanes, index64);
+    case TBE_TY_INT8: return nobag_kernel_lg<TBE_TY_INT8>(g.log2_lanes, index64);
+    case TBE_TY_INT4: return nobag_kernel_lg<TBE_TY_INT4>(g.log2_lanes, index64);
+    default:          return nobag_kernel_lg<TBE_TY_INT2>(g.log2_lanes, index64);
+  }
 }
 
 KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted, bool wide) {
@@ -416,8 +438,26 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     if (chunks > 0x7FFFFFFF) return fail(TBE_ERR_UNSUPPORTED, "too many indices for one launch");
     p.num_items = static_cast<int32_t>(chunks);
     p.order = nullptr;
-    const hipError_t err = launch(nobag_kernel, p, (chunks + kWavesPerBlock - 1) / kWavesPerBlock, false, s);
-    if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    const TbePlanSummary& plan = *a->plan;
+    if (plan.num_groups < 1 || plan.num_groups > TBE_MAX_GROUPS) return fail(TBE_ERR_INVALID_ARG, "bad plan");
+    // one launch per table group: 32-bit groups take their specialised kernel,
+    // which skips other tables' segments; tables beyond 32-bit addressing take
+    // the generic kernel
+    bool generic = false;
+    for (int gi = 0; gi < plan.num_groups; ++gi) {
+      const TbePlanGroup& g = plan.groups[gi];
+      if (!g.offset32) {
+        generic = true;
+        continue;
+      }
+      const hipError_t err = launch(nobag_kernel_group(g, p.index64 != 0), p,
+                                    (chunks + kWavesPerBlock - 1) / kWavesPerBlock, false, s);
+      if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    }
+    if (generic) {
+      const hipError_t err = launch(nobag_kernel, p, (chunks + kWavesPerBlock - 1) / kWavesPerBlock, false, s);
+      if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    }
     return TBE_OK;
   }
 
