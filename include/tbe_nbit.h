@@ -157,6 +157,7 @@ typedef struct TbeNbitArgs {
 #define TBE_FLAG_NO_XCD_REMAP 0x1  /* keep the hardware's round-robin block order */
 #define TBE_FLAG_NO_STREAM 0x2     /* never use the row-stream kernel (per-bag kernel for every group) */
 #define TBE_FLAG_FORCE_STREAM 0x4  /* row-stream kernel for every eligible group, whatever its size */
+#define TBE_FLAG_SERIAL_GROUPS 0x8 /* launch every table group on the caller's stream (no fork/join) */
 
 /*
  * Validate the table metadata and fill descs[T], table_order[T] (host memory)

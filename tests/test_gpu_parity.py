@@ -243,14 +243,15 @@ def test_double_table_forward_nobag(pkg, oracle, gpu, tables, out_ty):
 
 def test_c_abi_matches_torch_op(pkg, gpu):
     """The C ABI called directly (ctypes) gives the torch op's exact output, with and
-    without the XCD block renumbering."""
+    without the XCD block renumbering, and with the table groups on the caller's
+    stream instead of the two group streams."""
     from fbgemm_ascend_amd.workloads import make_workload
     for cid in (1, 3):
         wl = make_workload(cid, device=gpu, scale_rows=0.01, batch=256)
         m = wl.module
         _say(f"[gpu] c-abi cfg{cid}")
         a = wl.run()
-        for flags in (0, pkg.capi.TBE_FLAG_NO_XCD_REMAP):
+        for flags in (0, pkg.capi.TBE_FLAG_NO_XCD_REMAP, pkg.capi.TBE_FLAG_SERIAL_GROUPS):
             b = pkg.capi.forward_tensors(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets,
                                          wl.indices, wl.offsets, int(m.pooling_mode),
                                          wl.per_sample_weights, m.output_dtype, flags=flags)
