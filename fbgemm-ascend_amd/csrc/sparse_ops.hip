@@ -7,15 +7,17 @@
 //
 // Three phases, as in BA:142-231: count the indices of every (bucket, row)
 // segment, turn the counts into segment offsets with a device scan, scatter.  One
-// 64-wide wavefront owns one row at a time and walks its indices 64 per step.
-// For my_size <= 64 the row's per-bucket counters and write cursors live in one
-// VGPR (lane b = bucket b) and a lane's rank among the lower lanes of its bucket
-// comes from one ballot per bit of the bucket number (no pass per bucket, no
-// memory); larger my_size groups the lanes of a bucket with a ballot loop (one
-// pass per distinct bucket in the step) and advances in-memory counters with one
-// atomic per group.  Only the owning wave touches a row's counters,
-// so segments are filled in row order and the result is deterministic, including
-// for sequence = 0 where the reference's per-lane atomics (BK:582-584) leave the
+// 64-wide wavefront owns one row at a time and walks its indices in chunks of
+// kChunk x 64 (all loads of a chunk in flight at once); the row metadata of 64
+// rows is loaded together, one row per lane.  Buckets divide by a per-row
+// multiply-shift reciprocal.  For my_size <= 64 the count phase adds into a
+// per-wave LDS histogram, and the scatter phase counting-sorts each chunk by
+// bucket in LDS so that its stores run along segments; larger my_size groups the
+// lanes of a bucket with a ballot loop (one pass per distinct bucket in a step)
+// and advances in-memory counters with one atomic per group.  Only the owning
+// wave touches a row's counters and ranks follow index order, so segments are
+// filled in row order and the result is deterministic, including for
+// sequence = 0 where the reference's per-lane atomics (BK:582-584) leave the
 // order inside a segment unspecified.
 #include <hip/hip_runtime.h>
 
@@ -32,6 +34,7 @@ namespace tbe {
 namespace {
 
 constexpr int kWaveBB = 64;
+constexpr int kChunk = 8;                            // index loads in flight per wave
 constexpr int kBBBlock = 256;
 constexpr int kScanItems = 16;                       // elements per thread in the scan
 constexpr int kScanTile = kBBBlock * kScanItems;     // elements per scan work-group
@@ -59,7 +62,6 @@ struct BBParams {
   int64_t B;                    // rows per feature without batch_size_offsets
   int32_t F;
   int32_t keep;
-  int32_t bucket_bits;          // ceil(log2(my_size)) when my_size <= 64
 };
 
 __device__ __forceinline__ int64_t uni(int64_t v) {
@@ -68,41 +70,76 @@ __device__ __forceinline__ int64_t uni(int64_t v) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// What a wave needs to map the indices of one row (all values wave-uniform).
+// n / d for a wave-uniform 32-bit divisor d >= 1 by multiply and shift
+// (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, figure 4.1): l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1, q = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0)
+// with t = mulhi(m, n); exact for every 32-bit n.
+struct FastDiv32 {
+  uint32_t d, m, s1, s2;
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint32_t t = __umulhi(m, n);
+    return (t + ((n - t) >> s1)) >> s2;
+  }
+};
+
+__device__ __forceinline__ FastDiv32 make_fastdiv(uint32_t d) {
+  FastDiv32 f;
+  const uint32_t l = d > 1 ? 32u - static_cast<uint32_t>(__clz(static_cast<int>(d - 1))) : 0u;
+  f.d = d;
+  f.m = static_cast<uint32_t>(((static_cast<uint64_t>((uint64_t(1) << l) - d)) << 32) / d + 1);
+  f.s1 = l < 1 ? l : 1u;
+  f.s2 = l > 0 ? l - 1 : 0u;
+  return f;
+}
+
+// What a wave needs to map the indices of one row.  A wave computes these for
+// up to 64 of its rows at once, one row per lane (row_ctx_lane), and hands the
+// row it is about to walk to every lane with readlane (row_ctx_of), so the
+// offsets and per-feature loads of 64 rows share one memory round trip.
+// `fast` marks the rows whose indices below gsize take the 32-bit
+// multiply-shift division by lsize: no bucketize_pos, blk > 0, gsize < 2^32.
 template <typename IT>
 struct RowCtx {
   using UIT = std::make_unsigned_t<IT>;
   bool ok;
+  bool fast;
   int64_t s, e;
   IT blk;
   UIT gb, lbk, gsize, lsize, scalar;
   const IT* pos;
   int64_t pos_len;
+  FastDiv32 dl;
 };
 
-// BK:322-347 (row -> feature) and BK:388-421 (per-feature parameters).
+// BK:322-347 (row -> feature) and BK:388-421 (per-feature parameters) for row r
+// of this lane; r < 0 gives ok = false.
 template <typename IT, typename OT>
-__device__ __forceinline__ RowCtx<IT> row_ctx(const BBParams<IT, OT>& p, int64_t r) {
+__device__ __forceinline__ RowCtx<IT> row_ctx_lane(const BBParams<IT, OT>& p, int64_t r) {
   using UIT = std::make_unsigned_t<IT>;
   RowCtx<IT> c{};
+  c.ok = false;
+  if (r < 0) return c;
   int f;
   if (p.bso) {
     int lo = 0, hi = p.F;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (static_cast<int64_t>(uni(static_cast<int64_t>(p.bso[mid]))) <= r) lo = mid; else hi = mid - 1;
+      if (static_cast<int64_t>(p.bso[mid]) <= r) lo = mid; else hi = mid - 1;
     }
     f = lo;
   } else {
-    f = static_cast<int>(r / (p.B > 0 ? p.B : 1));
+    const uint64_t bdiv = static_cast<uint64_t>(p.B > 0 ? p.B : 1);
+    f = ((static_cast<uint64_t>(r) | bdiv) >> 32) == 0
+            ? static_cast<int>(static_cast<uint32_t>(r) / static_cast<uint32_t>(bdiv))
+            : static_cast<int>(static_cast<uint64_t>(r) / bdiv);
   }
-  c.ok = f >= 0 && f < p.F;
-  if (!c.ok) return c;
-  const IT blk = static_cast<IT>(uni(static_cast<int64_t>(p.block_sizes[f])));
-  c.ok = blk >= 0;
-  if (!c.ok) return c;
+  if (f < 0 || f >= p.F) return c;
+  const IT blk = p.block_sizes[f];
+  if (blk < 0) return c;
+  c.ok = true;
   const IT my = static_cast<IT>(p.my_size);
-  IT gb = p.tnb ? static_cast<IT>(uni(static_cast<int64_t>(p.tnb[f]))) : my;
+  IT gb = p.tnb ? p.tnb[f] : my;
   if (gb <= 0) gb = my;
   IT lbk = p.tnb ? static_cast<IT>(gb / my) : IT(1);
   if (lbk <= 0) lbk = 1;
@@ -114,8 +151,8 @@ __device__ __forceinline__ RowCtx<IT> row_ctx(const BBParams<IT, OT>& p, int64_t
   c.pos = nullptr;
   c.pos_len = 0;
   if (p.pos) {
-    c.pos = reinterpret_cast<const IT*>(uni(reinterpret_cast<int64_t>(p.pos[f])));
-    c.pos_len = uni(p.pos_len[f]);
+    c.pos = p.pos[f];
+    c.pos_len = p.pos_len[f];
     if (!c.pos || c.pos_len <= 0) {
       c.pos = nullptr;
       c.pos_len = 0;
@@ -123,12 +160,52 @@ __device__ __forceinline__ RowCtx<IT> row_ctx(const BBParams<IT, OT>& p, int64_t
   }
   c.scalar = 1;
   if (c.pos && blk == 0) c.scalar = static_cast<UIT>(static_cast<UIT>(c.pos[c.pos_len - 1]) / c.gb);
+  c.fast = !c.pos && blk > 0 && c.lsize > 0 && (static_cast<uint64_t>(c.gsize) >> 32) == 0 &&
+           (static_cast<uint64_t>(c.lsize) >> 32) == 0;
+  c.dl = make_fastdiv(c.fast ? static_cast<uint32_t>(c.lsize) : 1u);
   int64_t s = r == 0 ? 0 : static_cast<int64_t>(p.offsets[r - 1]);
   int64_t e = static_cast<int64_t>(p.offsets[r]);
-  s = std::min<int64_t>(std::max<int64_t>(uni(s), 0), p.N);  // malformed offsets never read out of bounds
-  e = std::min<int64_t>(std::max<int64_t>(uni(e), s), p.N);
+  s = std::min<int64_t>(std::max<int64_t>(s, 0), p.N);  // malformed offsets never read out of bounds
+  e = std::min<int64_t>(std::max<int64_t>(e, s), p.N);
   c.s = s;
   c.e = e;
+  return c;
+}
+
+__device__ __forceinline__ uint32_t rdl(uint32_t v, int j) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), j));
+}
+template <typename T>
+__device__ __forceinline__ T rdl_of(T v, int j) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = static_cast<uint64_t>(v);
+    return static_cast<T>((static_cast<uint64_t>(rdl(static_cast<uint32_t>(u >> 32), j)) << 32) |
+                          rdl(static_cast<uint32_t>(u), j));
+  } else {
+    return static_cast<T>(rdl(static_cast<uint32_t>(v), j));
+  }
+}
+
+// Lane j's row context, wave-uniform.
+template <typename IT>
+__device__ __forceinline__ RowCtx<IT> row_ctx_of(const RowCtx<IT>& m, int j) {
+  RowCtx<IT> c;
+  c.ok = rdl(m.ok ? 1u : 0u, j) != 0;
+  c.fast = rdl(m.fast ? 1u : 0u, j) != 0;
+  c.s = rdl_of(m.s, j);
+  c.e = rdl_of(m.e, j);
+  c.blk = rdl_of(m.blk, j);
+  c.gb = rdl_of(m.gb, j);
+  c.lbk = rdl_of(m.lbk, j);
+  c.gsize = rdl_of(m.gsize, j);
+  c.lsize = rdl_of(m.lsize, j);
+  c.scalar = rdl_of(m.scalar, j);
+  c.pos = reinterpret_cast<const IT*>(rdl_of(reinterpret_cast<uint64_t>(m.pos), j));
+  c.pos_len = rdl_of(m.pos_len, j);
+  c.dl.d = rdl(m.dl.d, j);
+  c.dl.m = rdl(m.dl.m, j);
+  c.dl.s1 = rdl(m.dl.s1, j);
+  c.dl.s2 = rdl(m.dl.s2, j);
   return c;
 }
 
@@ -183,6 +260,38 @@ __device__ __forceinline__ bool map_index(const RowCtx<IT>& c, std::make_unsigne
   return static_cast<uint64_t>(bucket) < my;
 }
 
+// Maps one step's index u of this lane (in: the lane holds an index of the row).
+// For rows marked fast, when no lane of the wave holds an index at or above
+// gsize (the wave-uniform common case), bucket = u / lsize and new index
+// u % lsize by the 32-bit multiply-shift division, without branches; otherwise
+// the general map_index.
+template <bool FAST, typename IT>
+__device__ __forceinline__ bool map_step(const RowCtx<IT>& c, bool in, std::make_unsigned_t<IT> u, uint64_t my,
+                                         bool keep, int64_t& bucket, IT& nidx) {
+  if constexpr (FAST) {
+    if (__builtin_amdgcn_ballot_w64(in && !(u < c.gsize)) == 0) {
+      const uint32_t n = static_cast<uint32_t>(u);
+      const uint32_t q = c.dl.div(n);
+      bucket = static_cast<int64_t>(q);
+      nidx = keep ? static_cast<IT>(u) : static_cast<IT>(n - q * c.dl.d);
+      return in && q < my;
+    }
+  }
+  return in && map_index<IT>(c, u, my, keep, bucket, nidx);
+}
+
+// The rows of one wave: each work-group takes a contiguous run of rows and its
+// waves interleave over it, so the group's waves walk neighbouring rows at the
+// same time (their segments of one bucket are neighbours in the output) and a
+// wave's rows mostly share one feature.
+__device__ __forceinline__ void wave_rows(int64_t L, int64_t& r0, int64_t& r1, int64_t& rs) {
+  const int64_t per = (L + gridDim.x - 1) / gridDim.x;
+  const int64_t b0 = std::min<int64_t>(blockIdx.x * per, L);
+  r0 = b0 + (threadIdx.x >> 6);
+  r1 = std::min<int64_t>(b0 + per, L);
+  rs = kBBBlock / kWaveBB;
+}
+
 // Integer add on an int32 / int64 counter (two's complement: the unsigned add is the same).
 __device__ __forceinline__ void add_count(int32_t* a, uint32_t v) { atomicAdd(reinterpret_cast<unsigned int*>(a), v); }
 __device__ __forceinline__ void add_count(int64_t* a, uint32_t v) {
@@ -195,31 +304,35 @@ __device__ __forceinline__ uint64_t lanes_below() {
   return (uint64_t(1) << lane_id()) - 1;  // lane 0: 0
 }
 
-// Bucket ranks without a pass per bucket (my_size <= 64): one ballot per bit of
-// the bucket number; the lanes whose bucket equals `key` are the valid lanes that
-// agree with `key` on every bit.
-constexpr int kMaxBucketBits = 6;
-
+// Bucket ranks without a pass per bucket (my_size <= 2^NB <= 64): one ballot
+// per bit of the bucket number; the lanes whose bucket equals `key` are the
+// valid lanes that agree with `key` on every bit.
+template <int NB>
 struct BucketBits {
   uint64_t valid;
-  uint64_t bit[kMaxBucketBits];
+  uint64_t bit[NB];
 };
 
-__device__ __forceinline__ BucketBits bucket_bits(bool valid, uint32_t bucket, int nbits) {
-  BucketBits r;
+template <int NB>
+__device__ __forceinline__ BucketBits<NB> bucket_bits(bool valid, uint32_t bucket) {
+  BucketBits<NB> r;
   r.valid = __builtin_amdgcn_ballot_w64(valid);
+  const uint32_t bv = valid ? bucket : 0u;  // invalid lanes set no bit
 #pragma unroll
-  for (int j = 0; j < kMaxBucketBits; ++j)
-    r.bit[j] = j < nbits ? __builtin_amdgcn_ballot_w64(valid && ((bucket >> j) & 1u)) : 0;
+  for (int j = 0; j < NB; ++j) r.bit[j] = __builtin_amdgcn_ballot_w64((bv >> j) & 1u);
   return r;
 }
 
-__device__ __forceinline__ uint64_t lanes_with_bucket(const BucketBits& bb, uint32_t key, int nbits) {
-  uint64_t m = bb.valid;
+template <int NB>
+__device__ __forceinline__ uint64_t lanes_with_bucket(const BucketBits<NB>& bb, uint32_t key) {
+  uint32_t lo = static_cast<uint32_t>(bb.valid), hi = static_cast<uint32_t>(bb.valid >> 32);
 #pragma unroll
-  for (int j = 0; j < kMaxBucketBits; ++j)
-    if (j < nbits) m &= ((key >> j) & 1u) ? bb.bit[j] : ~bb.bit[j];
-  return m;
+  for (int j = 0; j < NB; ++j) {
+    const uint32_t k = static_cast<uint32_t>(static_cast<int32_t>(key << (31 - j)) >> 31);  // bit j of key, all ones or zeros
+    lo &= ~(static_cast<uint32_t>(bb.bit[j]) ^ k);
+    hi &= ~(static_cast<uint32_t>(bb.bit[j] >> 32) ^ k);
+  }
+  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 template <typename T>
@@ -231,94 +344,218 @@ __global__ __launch_bounds__(kBBBlock) void bb_fill_zero(T* __restrict__ a, int6
 }
 
 // Phase 1 (BK:350-456): new_lengths[bucket * L + r] for every row r.  With
-// REG (my_size <= 64) lane b of one VGPR counts bucket b of the current row and
-// every row stores all its my_size counts; otherwise counts go to new_lengths
-// (zero-filled first) with one atomic per (step, bucket).
-template <typename IT, typename OT, bool REG>
-__global__ __launch_bounds__(kBBBlock) void bb_count(BBParams<IT, OT> p) {
+// REG (my_size <= 64) every index adds one to its bucket's slot of a per-wave
+// 64-entry LDS histogram (an LDS atomic, no return value) and every row stores
+// all its my_size counts; otherwise counts go to new_lengths (zero-filled first)
+// with one atomic per (step, bucket).  The next step's indices are loaded before
+// the current step is mapped, so every wave keeps two loads in flight.
+template <bool FAST, bool REG, typename IT, typename OT>
+__device__ __forceinline__ void count_row(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r, uint32_t* hist) {
   using UIT = std::make_unsigned_t<IT>;
-  const int64_t waves = static_cast<int64_t>(gridDim.x) * (kBBBlock / kWaveBB);
-  const int64_t w0 = blockIdx.x * static_cast<int64_t>(kBBBlock / kWaveBB) + (threadIdx.x >> 6);
-  for (int64_t r = w0; r < p.L; r += waves) {
-    const RowCtx<IT> c = row_ctx(p, r);
-    uint32_t cnt = 0;  // REG: this lane's bucket
-    if (c.ok) {
-      for (int64_t base = c.s; base < c.e; base += kWaveBB) {
-        const int64_t i = base + lane_id();
-        int64_t b = 0;
-        IT v;
-        bool valid = i < c.e && map_index<IT>(c, static_cast<UIT>(p.indices[i]), p.my_size, p.keep, b, v);
-        if constexpr (REG) {
-          // lane l counts the indices of bucket l
-          const BucketBits bb = bucket_bits(valid, static_cast<uint32_t>(b), p.bucket_bits);
-          cnt += static_cast<uint32_t>(__builtin_popcountll(lanes_with_bucket(bb, lane_id(), p.bucket_bits)));
-          continue;
-        }
-        uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
-        while (pending) {
-          const int leader = __builtin_ctzll(pending);
-          const int64_t bl = uni(__builtin_amdgcn_readlane(static_cast<int>(b), leader)) & 0xFFFFFFFFll;
-          const bool mine = valid && b == bl;
-          const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
-          const uint32_t k = static_cast<uint32_t>(__builtin_popcountll(m));
-          if (lane_id() == leader) add_count(p.new_lengths + bl * p.L + r, k);
-          pending &= ~m;
-          valid = valid && !mine;
-        }
-      }
-    }
+  const UIT* __restrict__ idx = reinterpret_cast<const UIT*>(p.indices);
+  for (int64_t chunk = c.s; chunk < c.e; chunk += kChunk * kWaveBB) {
+    UIT uk[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k)  // clamped, not branched: the row is not empty
+      uk[k] = idx[std::min<int64_t>(chunk + k * kWaveBB + lane_id(), c.e - 1)];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+    const int64_t base = chunk + k * kWaveBB;
+    if (base >= c.e) break;
+    const int64_t i = base + lane_id();
+    const UIT u = uk[k];
+    int64_t b = 0;
+    IT v;
+    bool valid = map_step<FAST, IT>(c, i < c.e, u, p.my_size, p.keep, b, v);
     if constexpr (REG) {
-      if (lane_id() < p.my_size) p.new_lengths[lane_id() * p.L + r] = static_cast<OT>(cnt);
-    }
-  }
-}
-
-// Phase 3 (BK:458-606 and 608-762): write every index to its segment, in row
-// order.  With REG lane b of one register holds the next write position of
-// bucket b of the current row; otherwise the cursors are per-segment counters in
-// the workspace, advanced with one atomic per (step, bucket).
-template <typename IT, typename OT, bool REG>
-__global__ __launch_bounds__(kBBBlock) void bb_scatter(BBParams<IT, OT> p) {
-  using UIT = std::make_unsigned_t<IT>;
-  const int64_t waves = static_cast<int64_t>(gridDim.x) * (kBBBlock / kWaveBB);
-  const int64_t w0 = blockIdx.x * static_cast<int64_t>(kBBBlock / kWaveBB) + (threadIdx.x >> 6);
-  for (int64_t r = w0; r < p.L; r += waves) {
-    const RowCtx<IT> c = row_ctx(p, r);
-    if (!c.ok) continue;
-    int64_t cur = 0;  // REG: write position of this lane's bucket
-    if constexpr (REG) {
-      if (lane_id() < p.my_size) cur = static_cast<int64_t>(p.new_offsets[lane_id() * p.L + r]);
-    }
-    for (int64_t base = c.s; base < c.e; base += kWaveBB) {
-      const int64_t i = base + lane_id();
-      int64_t b = 0;
-      IT v = 0;
-      const bool valid0 = i < c.e && map_index<IT>(c, static_cast<UIT>(p.indices[i]), p.my_size, p.keep, b, v);
-      bool valid = valid0;
-      int64_t w = 0;
-      uint64_t pending = 0;
-      if constexpr (REG) {
-        // rank among the lower lanes of the same bucket, after the bucket's cursor
-        // (lane b holds it); lane l then advances bucket l's cursor
-        const BucketBits bb = bucket_bits(valid0, static_cast<uint32_t>(b), p.bucket_bits);
-        const uint64_t mine = lanes_with_bucket(bb, static_cast<uint32_t>(b), p.bucket_bits);
-        const int src = static_cast<int>(b & 63) * 4;
-        const int64_t seg0 = static_cast<int64_t>(
-            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(cur >> 32)))) << 32) |
-            static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(cur & 0xFFFFFFFF))));
-        w = seg0 + __builtin_popcountll(mine & lanes_below());
-        cur += __builtin_popcountll(lanes_with_bucket(bb, lane_id(), p.bucket_bits));
-      } else {
-        pending = __builtin_amdgcn_ballot_w64(valid);
-      }
+      if (valid) atomicAdd(hist + static_cast<uint32_t>(b), 1u);
+    } else {
+      uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
       while (pending) {
         const int leader = __builtin_ctzll(pending);
         const int64_t bl = uni(__builtin_amdgcn_readlane(static_cast<int>(b), leader)) & 0xFFFFFFFFll;
         const bool mine = valid && b == bl;
         const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
         const uint32_t k = static_cast<uint32_t>(__builtin_popcountll(m));
+        if (lane_id() == leader) add_count(p.new_lengths + bl * p.L + r, k);
+        pending &= ~m;
+        valid = valid && !mine;
+      }
+    }
+    }
+  }
+}
+
+template <typename IT, typename OT, bool REG>
+__global__ __launch_bounds__(kBBBlock) void bb_count(BBParams<IT, OT> p) {
+  __shared__ uint32_t lds_hist[kBBBlock / kWaveBB][kWaveBB];
+  uint32_t* hist = lds_hist[threadIdx.x >> 6];
+  if constexpr (REG) hist[lane_id()] = 0;
+  int64_t r0, r1, rs;
+  wave_rows(p.L, r0, r1, rs);
+  for (int64_t g0 = r0; g0 < r1; g0 += kWaveBB * rs) {
+    const int64_t rl = g0 + lane_id() * rs;
+    const RowCtx<IT> mine = row_ctx_lane(p, rl < r1 ? rl : -1);
+    const int nrows = static_cast<int>(std::min<int64_t>(kWaveBB, (r1 - g0 + rs - 1) / rs));
+    for (int j = 0; j < nrows; ++j) {
+    const int64_t r = g0 + j * rs;
+    const RowCtx<IT> c = row_ctx_of(mine, j);
+    if (c.ok) {
+      if (c.fast) count_row<true, REG>(p, c, r, hist);
+      else count_row<false, REG>(p, c, r, hist);
+    }
+    if constexpr (REG) {
+      // the wave's LDS operations complete in order: the reads see every add
+      const uint32_t cnt = hist[lane_id()];
+      hist[lane_id()] = 0;
+      if (lane_id() < p.my_size) p.new_lengths[lane_id() * p.L + r] = static_cast<OT>(cnt);
+    }
+    }
+  }
+}
+
+// Phase 3 (BK:458-606 and 608-762): write every index to its segment, in row
+// order.
+//
+// my_size <= 64 (NB = ceil(log2 my_size) rounded up to 4 or 6): a wave walks its
+// row in chunks of up to kChunk * 64 indices and counting-sorts each chunk by
+// bucket in LDS before writing it, so consecutive lanes store consecutive
+// positions of one segment instead of 64 lanes hitting ~my_size segments:
+//   1. map every index, count the chunk's indices per bucket (LDS atomics);
+//   2. exclusive scan of the counts over the buckets (lane b = bucket b) gives
+//      each bucket's first slot in the chunk; the row's write cursor of bucket
+//      b (LDS, loaded from new_offsets at the row's first chunk) minus that
+//      slot is the slot -> output offset of bucket b;
+//   3. every index takes slot = first slot of its bucket + its rank among the
+//      chunk's earlier indices of that bucket (one ballot per bit of the bucket
+//      number; the highest lane of each bucket advances the bucket's slot);
+//   4. the wave writes the slots out in order, 64 at a time.
+// Ranks follow index order, so every segment keeps the row's order.
+//
+// my_size > 64: the cursors are per-segment counters in the workspace,
+// advanced with one atomic per (step, bucket), and indices are written in place.
+template <typename IT>
+struct ScatterStage {
+  IT v[kChunk * kWaveBB];         // new index of each slot
+  uint32_t meta[kChunk * kWaveBB];  // bucket | (position in the chunk << 8)
+  int64_t cur[kWaveBB];           // row's next output offset per bucket
+  int64_t delta[kWaveBB];         // output offset - slot, per bucket, this chunk
+  uint32_t cnt[kWaveBB];          // chunk count, then next slot, per bucket
+};
+
+__device__ __forceinline__ uint32_t wave_exclusive_scan(uint32_t x) {
+  uint32_t s = x;
+#pragma unroll
+  for (int d = 1; d < kWaveBB; d <<= 1) {
+    const uint32_t t = static_cast<uint32_t>(__shfl_up(static_cast<int>(s), d, kWaveBB));
+    if (lane_id() >= d) s += t;
+  }
+  return s - x;
+}
+
+template <bool FAST, int NB, typename IT, typename OT>
+__device__ __forceinline__ void scatter_row_staged(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r,
+                                                   ScatterStage<IT>& st) {
+  using UIT = std::make_unsigned_t<IT>;
+  constexpr uint32_t kNone = 0xFFu;
+  const UIT* __restrict__ idx = reinterpret_cast<const UIT*>(p.indices);
+  const int lane = lane_id();
+  for (int64_t chunk = c.s; chunk < c.e; chunk += kChunk * kWaveBB) {
+    UIT uk[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k)  // clamped, not branched: the row is not empty
+      uk[k] = idx[std::min<int64_t>(chunk + k * kWaveBB + lane, c.e - 1)];
+    // the row's cursors, loaded with its first indices (one wait for both)
+    if (chunk == c.s && lane < p.my_size) st.cur[lane] = static_cast<int64_t>(p.new_offsets[lane * p.L + r]);
+    // 1. map and count
+    uint32_t bk[kChunk];
+    IT vk[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      bk[k] = kNone;
+      vk[k] = 0;
+      const int64_t base = chunk + k * kWaveBB;
+      if (base < c.e) {
+        int64_t b = 0;
+        IT v = 0;
+        if (map_step<FAST, IT>(c, base + lane < c.e, uk[k], p.my_size, p.keep, b, v)) {
+          bk[k] = static_cast<uint32_t>(b);
+          vk[k] = v;
+          atomicAdd(&st.cnt[b], 1u);
+        }
+      }
+    }
+    // 2. first slot per bucket and slot -> output offset
+    const uint32_t n = st.cnt[lane];
+    const uint32_t first = wave_exclusive_scan(n);
+    const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(first + n), kWaveBB - 1));
+    const int64_t cu = st.cur[lane];
+    st.delta[lane] = cu - static_cast<int64_t>(first);
+    st.cur[lane] = cu + n;
+    st.cnt[lane] = first;
+    // 3. slots
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      if (chunk + k * kWaveBB >= c.e) break;
+      const bool valid = bk[k] != kNone;
+      const BucketBits<NB> bb = bucket_bits<NB>(valid, bk[k]);
+      const uint64_t mine = lanes_with_bucket<NB>(bb, bk[k]);
+      if (valid) {
+        // every lane reads before the highest lane of the bucket writes (in-order LDS)
+        const uint32_t slot = st.cnt[bk[k]] + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mine >> 32),
+                                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mine), 0u));
+        if ((mine >> lane) == 1) st.cnt[bk[k]] = slot + 1;
+        st.v[slot] = vk[k];
+        st.meta[slot] = bk[k] | (static_cast<uint32_t>(k * kWaveBB + lane) << 8);
+      }
+    }
+    // 4. write out in slot order
+    for (uint32_t t0 = 0; t0 < total; t0 += kWaveBB) {
+      const uint32_t t = t0 + static_cast<uint32_t>(lane);
+      if (t < total) {
+        const uint32_t m = st.meta[t];
+        const int64_t w = st.delta[m & 0xFFu] + t;
+        const int64_t i = chunk + (m >> 8);
+        if (w >= 0 && w < p.N) {
+          p.new_indices[w] = st.v[t];
+          if (p.new_weights) p.new_weights[w] = p.weights[i];
+          if (p.new_pos) p.new_pos[w] = static_cast<IT>(i - c.s);
+          if (p.unb) p.unb[i] = static_cast<IT>(w);
+        }
+      }
+    }
+    st.cnt[lane] = 0;
+  }
+}
+
+template <bool FAST, typename IT, typename OT>
+__device__ __forceinline__ void scatter_row_atomic(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r) {
+  using UIT = std::make_unsigned_t<IT>;
+  const UIT* __restrict__ idx = reinterpret_cast<const UIT*>(p.indices);
+  for (int64_t chunk = c.s; chunk < c.e; chunk += kChunk * kWaveBB) {
+    UIT uk[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k)  // clamped, not branched: the row is not empty
+      uk[k] = idx[std::min<int64_t>(chunk + k * kWaveBB + lane_id(), c.e - 1)];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      const int64_t base = chunk + k * kWaveBB;
+      if (base >= c.e) break;
+      const int64_t i = base + lane_id();
+      int64_t b = 0;
+      IT v = 0;
+      const bool valid0 = map_step<FAST, IT>(c, i < c.e, uk[k], p.my_size, p.keep, b, v);
+      int64_t w = 0;
+      bool valid = valid0;
+      uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
+      while (pending) {
+        const int leader = __builtin_ctzll(pending);
+        const int64_t bl = uni(__builtin_amdgcn_readlane(static_cast<int>(b), leader)) & 0xFFFFFFFFll;
+        const bool mine = valid && b == bl;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
+        const uint32_t cnt = static_cast<uint32_t>(__builtin_popcountll(m));
         uint32_t old = 0;
-        if (lane_id() == leader) old = atomicAdd(p.done + bl * p.L + r, k);
+        if (lane_id() == leader) old = atomicAdd(p.done + bl * p.L + r, cnt);
         old = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(old), leader));
         const int64_t seg0 = static_cast<int64_t>(p.new_offsets[bl * p.L + r]) + old;
         if (mine) w = seg0 + __builtin_popcountll(m & lanes_below());
@@ -330,6 +567,32 @@ __global__ __launch_bounds__(kBBBlock) void bb_scatter(BBParams<IT, OT> p) {
         if (p.new_weights) p.new_weights[w] = p.weights[i];
         if (p.new_pos) p.new_pos[w] = static_cast<IT>(i - c.s);
         if (p.unb) p.unb[i] = static_cast<IT>(w);
+      }
+    }
+  }
+}
+
+template <typename IT, typename OT, int NB>
+__global__ __launch_bounds__(kBBBlock) void bb_scatter(BBParams<IT, OT> p) {
+  __shared__ ScatterStage<IT> lds_stage[NB > 0 ? kBBBlock / kWaveBB : 1];
+  ScatterStage<IT>& st = lds_stage[NB > 0 ? (threadIdx.x >> 6) : 0];
+  if constexpr (NB > 0) st.cnt[lane_id()] = 0;
+  int64_t r0, r1, rs;
+  wave_rows(p.L, r0, r1, rs);
+  for (int64_t g0 = r0; g0 < r1; g0 += kWaveBB * rs) {
+    const int64_t rl = g0 + lane_id() * rs;
+    const RowCtx<IT> mine = row_ctx_lane(p, rl < r1 ? rl : -1);
+    const int nrows = static_cast<int>(std::min<int64_t>(kWaveBB, (r1 - g0 + rs - 1) / rs));
+    for (int j = 0; j < nrows; ++j) {
+      const int64_t r = g0 + j * rs;
+      const RowCtx<IT> c = row_ctx_of(mine, j);
+      if (!c.ok) continue;
+      if constexpr (NB > 0) {
+        if (c.fast) scatter_row_staged<true, NB>(p, c, r, st);
+        else scatter_row_staged<false, NB>(p, c, r, st);
+      } else {
+        if (c.fast) scatter_row_atomic<true>(p, c, r);
+        else scatter_row_atomic<false>(p, c, r);
       }
     }
   }
@@ -447,8 +710,8 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s) {
   p.B = a->batch_size_offsets ? 0 : a->lengths_size / a->num_features;
   p.F = a->num_features;
   p.keep = a->keep_orig_idx;
-  p.bucket_bits = 0;
-  while (p.bucket_bits < kMaxBucketBits && (int64_t(1) << p.bucket_bits) < a->my_size) ++p.bucket_bits;
+  int nbits = 0;  // ceil(log2(my_size))
+  while (nbits < 6 && (int64_t(1) << nbits) < a->my_size) ++nbits;
   const int64_t nseg = a->my_size * a->lengths_size;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -473,10 +736,10 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s) {
                      const_cast<const OT*>(p.new_lengths), nseg, const_cast<const OT*>(sums),
                      static_cast<OT*>(a->new_offsets));
   if (p.N > 0) {
-    if (reg)
-      hipLaunchKernelGGL((bb_scatter<IT, OT, true>), dim3(static_cast<uint32_t>(row_blocks)), dim3(kBBBlock), 0, s, p);
-    else
-      hipLaunchKernelGGL((bb_scatter<IT, OT, false>), dim3(static_cast<uint32_t>(row_blocks)), dim3(kBBBlock), 0, s, p);
+    const dim3 g(static_cast<uint32_t>(row_blocks));
+    if (!reg) hipLaunchKernelGGL((bb_scatter<IT, OT, 0>), g, dim3(kBBBlock), 0, s, p);
+    else if (nbits <= 4) hipLaunchKernelGGL((bb_scatter<IT, OT, 4>), g, dim3(kBBBlock), 0, s, p);
+    else hipLaunchKernelGGL((bb_scatter<IT, OT, 6>), g, dim3(kBBBlock), 0, s, p);
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));

@@ -44,7 +44,9 @@ extern "C" {
  * new_lengths, new_offsets), each 4 or 8.  Rows of a feature with a negative block
  * size, and indices whose bucket would fall outside [0, my_size) (only possible
  * with a total_num_blocks that is not a multiple of my_size), are left out; the
- * reference writes those out of bounds.
+ * reference writes those out of bounds.  Positions of new_indices, new_weights and
+ * new_pos past sum(new_lengths), and unbucketize_permute entries of left-out
+ * indices, are then not written.
  *
  * `workspace` is device scratch of tbe_block_bucketize_workspace_bytes() bytes.
  */

@@ -19,8 +19,10 @@ pytestmark = pytest.mark.gpu
 
 
 def _check(oracle, gpu, case, seed, *, weights=False, bucketize_pos=False, sequence=False, keep=False, tnb=None,
-           bspf=False, pos=False, via="fbgemm"):
+           bspf=False, pos=False, via="fbgemm", mutate=None):
     lengths, indices, block_sizes, w = gen_case(case, seed, weights)
+    if mutate is not None:
+        indices = mutate(indices)
     kw = {}
     if tnb:
         kw["total_num_blocks"] = gen_total_num_blocks(block_sizes, case.my_size, tnb, seed)
@@ -130,3 +132,73 @@ def test_bucketize_my_size_paths(pkg, oracle, gpu, my_size, sequence):
     case = Case(f"my{my_size}", 6, 50, 0, 150, 3, 9, my_size, np.int64)
     _check(oracle, gpu, case, my_size, weights=True, bucketize_pos=True, sequence=sequence)
     _check(oracle, gpu, case, my_size + 1, tnb="rand", sequence=sequence)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("my_size", [3, 16, 40])
+def test_bucketize_rows_over_several_chunks(pkg, oracle, gpu, dtype, my_size):
+    # rows of 400-1800 indices span several 512-index chunks of the scatter
+    # phase: the per-bucket cursors carry over from one chunk to the next
+    from _bucketize_cases import Case
+    case = Case(f"long_rows_my{my_size}", 4, 12, 400, 1800, 8, 40, my_size, dtype)
+    _check(oracle, gpu, case, 5 + my_size, weights=True, sequence=True)
+    _check(oracle, gpu, case, 6 + my_size, bucketize_pos=True, sequence=True, keep=True)
+    _check(oracle, gpu, case, 7 + my_size, weights=True, pos=True, sequence=True)
+
+
+def _beyond_blocks(dtype, my_size):
+    """About one index in ten moved at or above block_size * total_num_blocks
+    (int64: some at or above 2^32), so steps mix the multiply-shift division
+    with the general path."""
+    hi = np.iinfo(dtype).max
+
+    def mutate(ix):
+        rng = np.random.default_rng(my_size)
+        ix = ix.copy()
+        sel = rng.random(ix.size) < 0.1
+        big = rng.integers(0, hi, ix.size, dtype=np.int64, endpoint=False)
+        if dtype == np.int64:
+            big = np.where(rng.random(ix.size) < 0.5, big % (1 << 34), big)
+        ix[sel] = big[sel].astype(dtype)
+        return ix
+
+    return mutate
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("my_size", [5, 16, 100])
+@pytest.mark.parametrize("tnb", [None, "multiple"])
+def test_bucketize_indices_beyond_blocks(pkg, oracle, gpu, dtype, my_size, tnb):
+    # total_num_blocks absent or a multiple of my_size: every bucket of an index
+    # at or above the blocks, (idx % gb) / (gb / my_size), is below my_size
+    from _bucketize_cases import Case
+    case = Case(f"beyond_my{my_size}", 5, 40, 0, 200, 8, 40, my_size, dtype)
+    mutate = _beyond_blocks(dtype, my_size)
+    _check(oracle, gpu, case, 31, tnb=tnb, sequence=True, mutate=mutate)
+    _check(oracle, gpu, case, 32, tnb=tnb, weights=True, keep=True, mutate=mutate)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("my_size", [5, 100])
+def test_bucketize_bucket_past_my_size_dropped(pkg, oracle, gpu, dtype, my_size):
+    # total_num_blocks not a multiple of my_size and indices at or above the
+    # blocks give buckets >= my_size, for which the reference adds past the end
+    # of new_lengths (BK:455, undefined there).  Here such indices are left out:
+    # new_lengths and the filled prefix of new_indices / new_weights match the
+    # oracle, which leaves them out too; the tail past sum(new_lengths) is
+    # unwritten, as in the reference (at::empty, BA:156-157).
+    from _bucketize_cases import Case
+    case = Case(f"drop_my{my_size}", 5, 40, 0, 200, 8, 40, my_size, dtype)
+    lengths, indices, block_sizes, w = gen_case(case, 33, True)
+    indices = _beyond_blocks(dtype, my_size)(indices)
+    tnb = gen_total_num_blocks(block_sizes, my_size, "rand", 33)
+    want = oracle.block_bucketize_sparse_features(lengths, indices, False, False, block_sizes, my_size, weights=w,
+                                                  total_num_blocks=tnb)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    got = torch.ops.fbgemm.block_bucketize_sparse_features(d(lengths), d(indices), False, False, d(block_sizes),
+                                                           my_size, weights=d(w), total_num_blocks=d(tnb))
+    total = int(want[0].sum())
+    assert total < indices.size, "the case must drop some indices"
+    assert np.array_equal(got[0].cpu().numpy(), want[0])
+    assert np.array_equal(got[1].cpu().numpy()[:total], want[1][:total])
+    assert np.array_equal(got[2].cpu().numpy()[:total], want[2][:total])
