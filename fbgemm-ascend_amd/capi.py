@@ -23,6 +23,7 @@ TBE_FLAG_NO_XCD_REMAP = 0x1
 TBE_FLAG_NO_STREAM = 0x2
 TBE_FLAG_FORCE_STREAM = 0x4
 TBE_FLAG_SERIAL_GROUPS = 0x8
+TBE_FLAG_NARROW_WORDS = 0x10
 TBE_TABLE_OFFSET32 = 0x1
 TBE_TABLE_STREAM = 0x2
 

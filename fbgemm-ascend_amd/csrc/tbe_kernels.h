@@ -597,9 +597,9 @@ __device__ __forceinline__ WaveItems wave_items(const KParams& p) {
 // any is consumed: 16-32 rows in flight per wave for wide rows, a whole 64-index
 // chunk for short rows.  U*R always divides 64, so slot r0 + u*R + slot of a
 // step never passes lane 63 and slots past the bag read lanes holding kNoRow.
-template <int LG>
+template <int LG, int VW = 1>
 constexpr int unroll_for() {
-  return LG >= 5 ? 16 : (LG == 4 ? 8 : kWave / (kWave >> LG));
+  return LG >= 5 ? 16 / VW : (LG == 4 ? 8 : kWave / (kWave >> LG));
 }
 
 // A bag whose first index chunk has been requested: the kernels issue the index
@@ -718,10 +718,10 @@ __device__ __forceinline__ StagedBag stage_bag(const KParams& p, const WaveItems
 // finishes one element in each half of the lane pair, so after those levels a
 // lane holds E>>k fully-summed elements and every slot stores its share; the
 // slot bits below 4 are summed with DPP row rotations.
-template <int WT, int LG>
+template <int WT, int LG, int E = Traits<WT>::kEpd>
 __device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDesc& td, int L, int dw, bool col_ok,
-                                             int64_t b, const float (&acc)[Traits<WT>::kEpd], float bacc) {
-  constexpr int E = Traits<WT>::kEpd;
+                                             int64_t b, const float (&acc)[E], float bacc) {
+  constexpr int EW = Traits<WT>::kEpd;  // elements per word; E = EW x words per lane
   constexpr bool HDR = Traits<WT>::kHdr;
   constexpr bool S5 = LG <= 5 && E >= 2;
   constexpr int E1 = S5 ? E / 2 : E;
@@ -776,10 +776,10 @@ __device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDes
   float r[E2];
 #pragma unroll
   for (int e = 0; e < E2; ++e) {
-    const float x = HDR ? fmaf(a2[e], acc_post_scale<WT>(e0 + e), bacc) : a2[e];
+    const float x = HDR ? fmaf(a2[e], acc_post_scale<WT>((e0 + e) % EW), bacc) : a2[e];
     r[e] = p.mean ? x * scale : x;
   }
-  store_out<E2>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * E + e0, r);
+  store_out<E2>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * EW + e0, r);
 }
 
 // What a lane needs to gather rows of one bag's table.
@@ -791,12 +791,12 @@ struct BagCtx {
   bool col_ok;                // that word exists (rows narrower than the lanes)
 };
 
-template <int LG>
+template <int LG, int VW = 1>
 __device__ __forceinline__ BagCtx bag_ctx(const KParams& p, const StagedBag& sb) {
   BagCtx c;
   c.td = load_desc(p.tables + sb.t);
   const int lane = threadIdx.x & (kWave - 1);
-  c.dw = sb.ct * kWave + (lane & ((1 << LG) - 1));
+  c.dw = sb.ct * kWave + (lane & ((1 << LG) - 1)) * VW;
   c.col_ok = c.dw < c.td.data_dwords;
   c.col = static_cast<uint32_t>(c.td.data_offset + (c.col_ok ? 4 * c.dw : 0));
   c.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.weights + c.td.weights_offset), 0,
@@ -814,27 +814,46 @@ __device__ __forceinline__ uint32_t row_offset(const BagCtx& c, uint64_t idx, in
   return (lane < n && idx < rows) ? static_cast<uint32_t>(idx) * static_cast<uint32_t>(c.td.row_stride) : kNoRow;
 }
 
+// VW consecutive words at byte offset `off` of a buffer.
+template <int VW>
+__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&w)[VW]) {
+  if constexpr (VW == 1) {
+    w[0] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
+  } else if constexpr (VW == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(off), 0, 0);
+    w[0] = v[0];
+    w[1] = v[1];
+  } else {
+    static_assert(VW == 4, "1, 2 or 4 words per lane");
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0);
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+    w[3] = v[3];
+  }
+}
+
 // Registers of one gather step: U rows per lane slot.
-template <int U>
+template <int U, int VW = 1>
 struct StepRegs {
-  uint32_t d[U], h[U];
+  uint32_t d[U][VW], h[U];
   float w[U];
 };
 
 // Issue the loads of step `st` of a chunk (rows st*R*U .. st*R*U + R*U - 1).
 // Slot st*R*U + u*R + slot < 64 because R*U divides 64; slots past the chunk
 // read lanes that hold kNoRow and load zero.
-template <int WT, int LG, bool WEIGHTED>
+template <int WT, int LG, bool WEIGHTED, int VW>
 __device__ __forceinline__ void issue_step(const BagCtx& c, uint32_t my_off, float my_w, int st,
-                                           StepRegs<unroll_for<LG>()>& r) {
+                                           StepRegs<unroll_for<LG, VW>(), VW>& r) {
   constexpr int R = kWave >> LG;
-  constexpr int U = unroll_for<LG>();
+  constexpr int U = unroll_for<LG, VW>();
   const int slot4 = ((threadIdx.x & (kWave - 1)) >> LG) * 4;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int src = (st * R * U + u * R) * 4 + slot4;
     const uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
-    r.d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(c.rs, static_cast<int>(off + c.col), 0, 0));
+    load_words<VW>(c.rs, off + c.col, r.d[u]);
     if constexpr (Traits<WT>::kHdr) r.h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(c.rs, static_cast<int>(off), 0, 0));
     else r.h[u] = 0u;
     if constexpr (WEIGHTED) r.w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
@@ -842,30 +861,38 @@ __device__ __forceinline__ void issue_step(const BagCtx& c, uint32_t my_off, flo
   }
 }
 
-template <int WT, int LG, bool WEIGHTED>
-__device__ __forceinline__ void consume_step(const KParams& p, const StepRegs<unroll_for<LG>()>& r, int st, int n,
-                                             float (&acc)[Traits<WT>::kEpd], float& bacc) {
+template <int WT, int LG, bool WEIGHTED, int VW>
+__device__ __forceinline__ void consume_step(const KParams& p, const StepRegs<unroll_for<LG, VW>(), VW>& r, int st, int n,
+                                             float (&acc)[Traits<WT>::kEpd * VW], float& bacc) {
   constexpr int R = kWave >> LG;
-  constexpr int U = unroll_for<LG>();
+  constexpr int U = unroll_for<LG, VW>();
+  constexpr int EW = Traits<WT>::kEpd;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (st * R * U + u * R < n) accum_row<WT, WEIGHTED>(acc, bacc, r.d[u], r.h[u], r.w[u], p.fp8);  // wave-uniform
+    if (st * R * U + u * R < n) {  // wave-uniform
+#pragma unroll
+      for (int v = 0; v < VW; ++v) {  // the row's bias once, with its first word
+        float unused = 0.f;
+        accum_row<WT, WEIGHTED>(*reinterpret_cast<float(*)[EW]>(&acc[v * EW]), v == 0 ? bacc : unused, r.d[u][v],
+                                r.h[u], r.w[u], p.fp8);
+      }
+    }
   }
 }
 
 // Steps st0.. of one chunk of <= 64 indices, each issued then consumed.
-template <int WT, int LG, bool WEIGHTED>
+template <int WT, int LG, bool WEIGHTED, int VW>
 __device__ __forceinline__ void pool_steps(const KParams& p, const BagCtx& c, uint32_t my_off, float my_w, int n,
-                                           int st0, float (&acc)[Traits<WT>::kEpd], float& bacc) {
-  constexpr int kSteps = kWave / ((kWave >> LG) * unroll_for<LG>());
+                                           int st0, float (&acc)[Traits<WT>::kEpd * VW], float& bacc) {
+  constexpr int kSteps = kWave / ((kWave >> LG) * unroll_for<LG, VW>());
 #pragma unroll
   for (int st = 1; st < kSteps; ++st) {
     if (st >= st0 && st * (kWave / kSteps) < n) {  // wave-uniform
-      StepRegs<unroll_for<LG>()> r;
-      issue_step<WT, LG, WEIGHTED>(c, my_off, my_w, st, r);
+      StepRegs<unroll_for<LG, VW>(), VW> r;
+      issue_step<WT, LG, WEIGHTED, VW>(c, my_off, my_w, st, r);
       // keep the step's loads together, ahead of the guarded accumulations
       __builtin_amdgcn_sched_barrier(0);
-      consume_step<WT, LG, WEIGHTED>(p, r, st, n, acc, bacc);
+      consume_step<WT, LG, WEIGHTED, VW>(p, r, st, n, acc, bacc);
     }
   }
 }
@@ -873,30 +900,30 @@ __device__ __forceinline__ void pool_steps(const KParams& p, const BagCtx& c, ui
 // Finish a bag whose step 0 rows are in `r0`: consume them, gather the rest of
 // the bag (longer than one step or one chunk), reduce and store (P:44-85 bag
 // walk, P:282-315 pooling, P:346-394 chunked bag, P:319-342 store).
-template <int WT, int LG, typename IndexT, bool WEIGHTED>
+template <int WT, int LG, typename IndexT, bool WEIGHTED, int VW>
 __device__ __forceinline__ void finish_bag_fast(const KParams& p, const StagedBag& sb, const BagCtx& c,
-                                                uint32_t my_off, const StepRegs<unroll_for<LG>()>& r0) {
-  constexpr int E = Traits<WT>::kEpd;
+                                                uint32_t my_off, const StepRegs<unroll_for<LG, VW>(), VW>& r0) {
+  constexpr int E = Traits<WT>::kEpd * VW;
   float acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
   float bacc = 0.f;
   const int L = sb.L;
   const int n0 = min(L, kWave);
-  consume_step<WT, LG, WEIGHTED>(p, r0, 0, n0, acc, bacc);
-  pool_steps<WT, LG, WEIGHTED>(p, c, my_off, sb.w, n0, 1, acc, bacc);
+  consume_step<WT, LG, WEIGHTED, VW>(p, r0, 0, n0, acc, bacc);
+  pool_steps<WT, LG, WEIGHTED, VW>(p, c, my_off, sb.w, n0, 1, acc, bacc);
   for (int base = kWave; base < L; base += kWave) {
     const int n = min(kWave, L - base);
     const uint64_t idx = load_index_chunk<IndexT>(p, sb.start + base, n);
     const float w = WEIGHTED ? load_weight_chunk(p, sb.start + base, n) : 0.f;
     const uint32_t off = row_offset(c, idx, n);
-    StepRegs<unroll_for<LG>()> r;
-    issue_step<WT, LG, WEIGHTED>(c, off, w, 0, r);
+    StepRegs<unroll_for<LG, VW>(), VW> r;
+    issue_step<WT, LG, WEIGHTED, VW>(c, off, w, 0, r);
     __builtin_amdgcn_sched_barrier(0);
-    consume_step<WT, LG, WEIGHTED>(p, r, 0, n, acc, bacc);
-    pool_steps<WT, LG, WEIGHTED>(p, c, off, w, n, 1, acc, bacc);
+    consume_step<WT, LG, WEIGHTED, VW>(p, r, 0, n, acc, bacc);
+    pool_steps<WT, LG, WEIGHTED, VW>(p, c, off, w, n, 1, acc, bacc);
   }
-  if (sb.valid) reduce_store<WT, LG>(p, c.td, L, c.dw, c.col_ok, sb.b, acc, bacc);
+  if (sb.valid) reduce_store<WT, LG, E>(p, c.td, L, c.dw, c.col_ok, sb.b, acc, bacc);
 }
 
 // ---------------------------------------------------------------- pooled bag, 64-bit tables
@@ -1011,6 +1038,17 @@ template <int WT, int LG>
 constexpr int stream_vw() {
   return stream_vw_for(Traits<WT>::kEpd, LG);
 }
+// Words per lane of the per-bag kernel.  Two words (8 bytes) for INT4 rows of
+// 17-32 payload words: the row then takes 16 lanes, a load instruction reaches 4
+// rows instead of 2, and a lane's 16 elements share one row's address and weight
+// work (config 3's INT4 D=256 tables: 148 -> 105 us).  Measured and kept at one
+// word elsewhere: 16-word rows (INT4/INT8/FP16, 3-10 % slower), INT8 and FP16
+// rows of 17-32 words (no gain or up to 6 % slower), 33-64-word rows (15-40 %
+// slower at 2 words: the register ring halves occupancy).
+template <int WT, int LG>
+constexpr int fast_vw() {
+  return (LG == 5 && WT == TBE_TY_INT4) ? 2 : 1;
+}
 inline int stream_vw_of(int weight_ty, int lg) {
   static const int epw[] = {1, 2, 4, 8, 16, 2, 4};  // elements per word by TbeSparseType
   return stream_vw_for(epw[weight_ty], lg);
@@ -1045,24 +1083,6 @@ __device__ __forceinline__ uint32_t slot_bcast(uint32_t v) {
   }
 }
 
-// VW consecutive words at byte offset `off` of a buffer.
-template <int VW>
-__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&w)[VW]) {
-  if constexpr (VW == 1) {
-    w[0] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
-  } else if constexpr (VW == 2) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(off), 0, 0);
-    w[0] = v[0];
-    w[1] = v[1];
-  } else {
-    static_assert(VW == 4, "1, 2 or 4 words per lane");
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0);
-    w[0] = v[0];
-    w[1] = v[1];
-    w[2] = v[2];
-    w[3] = v[3];
-  }
-}
 
 // Entry l mod C of a slot's index chunk starting at position q0 (-1 past the
 // slot's run) and its per-sample weight.  The raw index is kept until the chunk
@@ -1377,9 +1397,11 @@ __global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
 // Software pipeline over the wave's items: while bag i is consumed, the rows of
 // bag i+1 are in flight and the index chunk of bag i+2 is being fetched.  The
 // loop body is unrolled twice so the two row buffers swap roles without copies.
-template <int WT, int LG, typename IndexT, bool WEIGHTED>
+template <int WT, int LG, typename IndexT, bool WEIGHTED, int VW>
 __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
-  constexpr int U = unroll_for<LG>();
+  // VW words per lane: 2^LGE lanes cover a row's 2^LG words of this column tile
+  constexpr int LGE = VW == 2 ? LG - 1 : LG;
+  constexpr int U = unroll_for<LGE, VW>();
   const WaveItems w = wave_items(p);
   if (w.first >= w.end) return;
   const uint32_t nitems = (w.end - w.first + w.step - 1) / w.step;
@@ -1387,17 +1409,17 @@ __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
   uint32_t g = 0;
   StagedBag s0 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, 0);
   StagedBag s1 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, 1);
-  BagCtx c0 = bag_ctx<LG>(p, s0);
+  BagCtx c0 = bag_ctx<LGE, VW>(p, s0);
   uint32_t off0 = row_offset(c0, s0.idx, min(s0.L, kWave));
-  StepRegs<U> ra, rb;
-  issue_step<WT, LG, WEIGHTED>(c0, off0, s0.w, 0, ra);
+  StepRegs<U, VW> ra, rb;
+  issue_step<WT, LGE, WEIGHTED, VW>(c0, off0, s0.w, 0, ra);
   while (true) {
     StagedBag s2 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, g + 2);
-    BagCtx c1 = bag_ctx<LG>(p, s1);
+    BagCtx c1 = bag_ctx<LGE, VW>(p, s1);
     uint32_t off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
-    issue_step<WT, LG, WEIGHTED>(c1, off1, s1.w, 0, rb);
+    issue_step<WT, LGE, WEIGHTED, VW>(c1, off1, s1.w, 0, rb);
     __builtin_amdgcn_sched_barrier(0);
-    finish_bag_fast<WT, LG, IndexT, WEIGHTED>(p, s0, c0, off0, ra);
+    finish_bag_fast<WT, LGE, IndexT, WEIGHTED, VW>(p, s0, c0, off0, ra);
     if (++g >= nitems) break;
     s0 = s1;
     c0 = c1;
@@ -1405,11 +1427,11 @@ __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
     s1 = s2;
 
     s2 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, g + 2);
-    c1 = bag_ctx<LG>(p, s1);
+    c1 = bag_ctx<LGE, VW>(p, s1);
     off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
-    issue_step<WT, LG, WEIGHTED>(c1, off1, s1.w, 0, ra);
+    issue_step<WT, LGE, WEIGHTED, VW>(c1, off1, s1.w, 0, ra);
     __builtin_amdgcn_sched_barrier(0);
-    finish_bag_fast<WT, LG, IndexT, WEIGHTED>(p, s0, c0, off0, rb);
+    finish_bag_fast<WT, LGE, IndexT, WEIGHTED, VW>(p, s0, c0, off0, rb);
     if (++g >= nitems) break;
     s0 = s1;
     c0 = c1;
@@ -1445,22 +1467,33 @@ __global__ __launch_bounds__(kBlock) void pooled_wide_kernel(KParams p) {
 
 using KernelFn = void (*)(KParams);
 
-template <int WT, int LG>
-KernelFn fast_kernel_for(bool index64, bool weighted) {
-  if (index64) return weighted ? pooled_fast_kernel<WT, LG, int64_t, true> : pooled_fast_kernel<WT, LG, int64_t, false>;
-  return weighted ? pooled_fast_kernel<WT, LG, int32_t, true> : pooled_fast_kernel<WT, LG, int32_t, false>;
+template <int WT, int LG, int VW>
+KernelFn fast_kernel_vw(bool index64, bool weighted) {
+  if (index64)
+    return weighted ? pooled_fast_kernel<WT, LG, int64_t, true, VW> : pooled_fast_kernel<WT, LG, int64_t, false, VW>;
+  return weighted ? pooled_fast_kernel<WT, LG, int32_t, true, VW> : pooled_fast_kernel<WT, LG, int32_t, false, VW>;
 }
 
+template <int WT, int LG>
+KernelFn fast_kernel_for(bool index64, bool weighted, bool wide_words) {
+  if constexpr (fast_vw<WT, LG>() == 2) {
+    if (wide_words) return fast_kernel_vw<WT, LG, 2>(index64, weighted);
+  }
+  return fast_kernel_vw<WT, LG, 1>(index64, weighted);
+}
+
+// wide_words: every table of the group has an even number of payload words
+// (TBE_TABLE_STREAM), so lanes may read two words at a time.
 template <int WT>
-KernelFn fast_kernel_lg(int lg, bool index64, bool weighted) {
+KernelFn fast_kernel_lg(int lg, bool index64, bool weighted, bool wide_words) {
   switch (lg) {
-    case 0: return fast_kernel_for<WT, 0>(index64, weighted);
-    case 1: return fast_kernel_for<WT, 1>(index64, weighted);
-    case 2: return fast_kernel_for<WT, 2>(index64, weighted);
-    case 3: return fast_kernel_for<WT, 3>(index64, weighted);
-    case 4: return fast_kernel_for<WT, 4>(index64, weighted);
-    case 5: return fast_kernel_for<WT, 5>(index64, weighted);
-    default: return fast_kernel_for<WT, 6>(index64, weighted);
+    case 0: return fast_kernel_for<WT, 0>(index64, weighted, wide_words);
+    case 1: return fast_kernel_for<WT, 1>(index64, weighted, wide_words);
+    case 2: return fast_kernel_for<WT, 2>(index64, weighted, wide_words);
+    case 3: return fast_kernel_for<WT, 3>(index64, weighted, wide_words);
+    case 4: return fast_kernel_for<WT, 4>(index64, weighted, wide_words);
+    case 5: return fast_kernel_for<WT, 5>(index64, weighted, wide_words);
+    default: return fast_kernel_for<WT, 6>(index64, weighted, wide_words);
   }
 }
 

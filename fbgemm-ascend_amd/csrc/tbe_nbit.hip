@@ -16,25 +16,25 @@
 namespace tbe {
 
 // instantiated once, in tbe_kern_<type>.hip
-extern template KernelFn fast_kernel_lg<TBE_TY_FP32>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_FP32>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP32>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_FP32>(int, bool);
-extern template KernelFn fast_kernel_lg<TBE_TY_FP16>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_FP16>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP16>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_FP16>(int, bool);
-extern template KernelFn fast_kernel_lg<TBE_TY_BF16>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_BF16>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_BF16>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_BF16>(int, bool);
-extern template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP8>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool);
-extern template KernelFn fast_kernel_lg<TBE_TY_INT8>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_INT8>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT8>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_INT8>(int, bool);
-extern template KernelFn fast_kernel_lg<TBE_TY_INT4>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_INT4>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT4>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_INT4>(int, bool);
-extern template KernelFn fast_kernel_lg<TBE_TY_INT2>(int, bool, bool);
+extern template KernelFn fast_kernel_lg<TBE_TY_INT2>(int, bool, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT2>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_INT2>(int, bool);
 
@@ -218,16 +218,16 @@ KernelFn nobag_kernel_group(const TbePlanGroup& g, bool index64) {
   }
 }
 
-KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted, bool wide) {
+KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted, bool wide, bool wide_words) {
   if (wide || !g.offset32) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
   switch (g.weight_ty) {
-    case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64, weighted);
-    case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64, weighted);
-    case TBE_TY_BF16: return fast_kernel_lg<TBE_TY_BF16>(g.log2_lanes, index64, weighted);
-    case TBE_TY_FP8:  return fast_kernel_lg<TBE_TY_FP8>(g.log2_lanes, index64, weighted);
-    case TBE_TY_INT8: return fast_kernel_lg<TBE_TY_INT8>(g.log2_lanes, index64, weighted);
-    case TBE_TY_INT4: return fast_kernel_lg<TBE_TY_INT4>(g.log2_lanes, index64, weighted);
-    default:          return fast_kernel_lg<TBE_TY_INT2>(g.log2_lanes, index64, weighted);
+    case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64, weighted, wide_words);
+    case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64, weighted, wide_words);
+    case TBE_TY_BF16: return fast_kernel_lg<TBE_TY_BF16>(g.log2_lanes, index64, weighted, wide_words);
+    case TBE_TY_FP8:  return fast_kernel_lg<TBE_TY_FP8>(g.log2_lanes, index64, weighted, wide_words);
+    case TBE_TY_INT8: return fast_kernel_lg<TBE_TY_INT8>(g.log2_lanes, index64, weighted, wide_words);
+    case TBE_TY_INT4: return fast_kernel_lg<TBE_TY_INT4>(g.log2_lanes, index64, weighted, wide_words);
+    default:          return fast_kernel_lg<TBE_TY_INT2>(g.log2_lanes, index64, weighted, wide_words);
   }
 }
 
@@ -544,7 +544,9 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     } else {
       const int64_t items = static_cast<int64_t>(g.count) * a->B * g.col_tiles;
       p.num_items = static_cast<int32_t>(items);
-      err = launch(pooled_kernel_for(g, p.index64 != 0, weighted, wide), p,
+      // two words per lane when every table of the group has an even word count
+      const bool wide_words = g.stream && !(a->flags & TBE_FLAG_NARROW_WORDS);
+      err = launch(pooled_kernel_for(g, p.index64 != 0, weighted, wide, wide_words), p,
                    (items + kWavesPerBlock - 1) / kWavesPerBlock, true, gstream);
     }
     if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));

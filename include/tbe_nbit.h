@@ -77,8 +77,9 @@ typedef struct TbeTableDesc {
  * (buffer loads with range checking). */
 #define TBE_TABLE_OFFSET32 0x1
 /* TbeTableDesc.flags: OFFSET32 and a payload of at least 8 words in an even
- * number of words, so the table is gathered by the row-stream kernel (8-byte
- * lanes, one contiguous index run per slot of lanes). */
+ * number of words, so the table may be gathered by the row-stream kernel (8-byte
+ * lanes, one contiguous index run per slot of lanes) and, for INT4 rows of 17-32
+ * words, by the per-bag kernel with 8-byte lanes. */
 #define TBE_TABLE_STREAM 0x2
 
 /* Host-side table metadata handed to the planner (all host pointers). */
@@ -158,6 +159,7 @@ typedef struct TbeNbitArgs {
 #define TBE_FLAG_NO_STREAM 0x2     /* never use the row-stream kernel (per-bag kernel for every group) */
 #define TBE_FLAG_FORCE_STREAM 0x4  /* row-stream kernel for every eligible group, whatever its size */
 #define TBE_FLAG_SERIAL_GROUPS 0x8 /* launch every table group on the caller's stream (no fork/join) */
+#define TBE_FLAG_NARROW_WORDS 0x10 /* per-bag kernel: one 4-byte word per lane, also for rows of 16+ words */
 
 /*
  * Validate the table metadata and fill descs[T], table_order[T] (host memory)

@@ -210,6 +210,26 @@ def test_random_multi_table_forward_types(pkg, oracle, gpu, T, ty, pm, weighted,
                   flags=flags)
 
 
+# INT4 rows of 17-32 payload words: tables with an even word count read two words
+# per lane in the per-bag kernel, odd ones (D=136, 248) one; mixed in one call
+# they form two groups.  TBE_FLAG_NARROW_WORDS keeps one word per lane.
+INT4_WIDE_TABLES = [[(3000, 256), (2000, 192)], [(3000, 144), (2000, 136), (1000, 248), (500, 256)],
+                    [(20000, 240)]]
+
+
+@pytest.mark.parametrize("words", ["default", "narrow"])
+@pytest.mark.parametrize("tables", list(range(len(INT4_WIDE_TABLES))))
+@pytest.mark.parametrize("pm,weighted,out_ty", [(0, False, FP16), (1, True, FP32), (0, True, BF16), (1, False, FP16)])
+def test_int4_wide_word_lanes(pkg, oracle, gpu, tables, pm, weighted, out_ty, words):
+    tabs = INT4_WIDE_TABLES[tables]
+    seed = 0x44 + 7 * tables + 3 * pm + int(weighted)
+    m, idx, off, psw = _random_case(pkg, gpu, seed, len(tabs), INT4, pm, weighted, torch.int32, out_ty, B=97,
+                                    tables=tabs, L_list=[1 + (13 * k + seed) % 150 for k in range(len(tabs))])
+    flags = pkg.capi.TBE_FLAG_NARROW_WORDS if words == "narrow" else 0
+    _check_module(oracle, m, idx, off, psw, f"int4 wide {tabs} pm={pm} w={weighted} out={out_ty} {words}",
+                  flags=flags)
+
+
 BAG_TABLES = [[(1000, 16), (2000, 16)], [(2000, 256), (1000, 256)], [(2000, 512), (1000, 512)],
               [(2000, 1024), (1000, 1024)], [(2000, 2048), (1000, 2048)], [(2000, 4096), (1000, 4096)],
               [(2000, 16), (1000, 256)], [(2000, 16), (1000, 512)], [(2000, 16), (1000, 1024)],
