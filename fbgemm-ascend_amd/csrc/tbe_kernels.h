@@ -254,7 +254,13 @@ __device__ __forceinline__ void decode(uint32_t d, float (&v)[Traits<WT>::kEpd],
 template <int WT>
 __device__ __forceinline__ float acc_post_scale(int e) {
   if constexpr (WT == TBE_TY_INT4) return (e & 1) ? 1048576.0f : 16777216.0f;
-  return (WT == TBE_TY_INT8 || WT == TBE_TY_INT2) ? 16777216.0f : 1.0f;
+  if constexpr (WT == TBE_TY_INT2) {
+    // field j of a half-word reads as 4^j' x 2^-24 (j' = j for j < 5, j - 5 after the 10-bit shift)
+    const int j = e & 7;
+    const int jp = j < 5 ? j : j - 5;
+    return __int_as_float((127 + 24 - 2 * jp) << 23);
+  }
+  return WT == TBE_TY_INT8 ? 16777216.0f : 1.0f;
 }
 
 // Add one row's contribution: acc[e] += w * value[e] (value = scale*q + bias for INT
@@ -294,10 +300,14 @@ __device__ __forceinline__ void accum_row(float (&acc)[Traits<WT>::kEpd], float&
       acc[6] = fmaf(h16hi(p2), s, acc[6]);
       acc[3] = fmaf(h16lo(p3), s, acc[3]);
       acc[7] = fmaf(h16hi(p3), s, acc[7]);
-    } else {  // INT2: 2-bit fields j and j+8 are elements j and j+8
+    } else {  // INT2: 2-bit fields j and j+8 of the halves are elements j and j+8
+      // fields 0-4 are masked in place (a subnormal half's mantissa holds bits 0-9:
+      // value 4^j x field x 2^-24), fields 5-7 after one 10-bit shift; acc_post_scale
+      // removes the 4^j'
+      const uint32_t d10 = d >> 10;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint32_t pj = (d >> (2 * j)) & 0x00030003u;
+        const uint32_t pj = j < 5 ? (d & (0x00030003u << (2 * j))) : (d10 & (0x00030003u << (2 * (j - 5))));
         acc[j] = fmaf(h16lo(pj), s, acc[j]);
         acc[j + 8] = fmaf(h16hi(pj), s, acc[j + 8]);
       }
