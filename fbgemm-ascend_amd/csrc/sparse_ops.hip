@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kWaveBB = 64;
 constexpr int kChunk = 8;                            // index loads in flight per wave
+constexpr int kRsrcWord3 = 0x00020000;               // raw buffer resource word 3 (gfx9: 32-bit data, no swizzle)
 constexpr int kBBBlock = 256;
 constexpr int kScanItems = 16;                       // elements per thread in the scan
 constexpr int kScanTile = kBBBlock * kScanItems;     // elements per scan work-group
@@ -347,47 +348,83 @@ __global__ __launch_bounds__(kBBBlock) void bb_fill_zero(T* __restrict__ a, int6
 // REG (my_size <= 64) every index adds one to its bucket's slot of a per-wave
 // 64-entry LDS histogram (an LDS atomic, no return value) and every row stores
 // all its my_size counts; otherwise counts go to new_lengths (zero-filled first)
-// with one atomic per (step, bucket).  The next step's indices are loaded before
-// the current step is mapped, so every wave keeps two loads in flight.
+// with one atomic per (step, bucket).  A row's indices are read in chunks of
+// kChunk x 64 with all loads of a chunk in flight; with REG the first chunk of
+// the next row loads while the current row is counted.
 template <bool FAST, bool REG, typename IT, typename OT>
-__device__ __forceinline__ void count_row(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r, uint32_t* hist) {
+__device__ __forceinline__ void count_row(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r, uint32_t* hist,
+                                          const std::make_unsigned_t<IT> (*first)[kChunk]) {
   using UIT = std::make_unsigned_t<IT>;
   const UIT* __restrict__ idx = reinterpret_cast<const UIT*>(p.indices);
-  for (int64_t chunk = c.s; chunk < c.e; chunk += kChunk * kWaveBB) {
+  auto count_chunk = [&](int64_t chunk, const UIT (&uk)[kChunk]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+      const int64_t base = chunk + k * kWaveBB;
+      if (base >= c.e) break;
+      const int64_t i = base + lane_id();
+      int64_t b = 0;
+      IT v;
+      bool valid = map_step<FAST, IT>(c, i < c.e, uk[k], p.my_size, p.keep, b, v);
+      if constexpr (REG) {
+        if (valid) atomicAdd(hist + static_cast<uint32_t>(b), 1u);
+      } else {
+        uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
+        while (pending) {
+          const int leader = __builtin_ctzll(pending);
+          const int64_t bl = uni(__builtin_amdgcn_readlane(static_cast<int>(b), leader)) & 0xFFFFFFFFll;
+          const bool mine = valid && b == bl;
+          const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
+          const uint32_t n = static_cast<uint32_t>(__builtin_popcountll(m));
+          if (lane_id() == leader) add_count(p.new_lengths + bl * p.L + r, n);
+          pending &= ~m;
+          valid = valid && !mine;
+        }
+      }
+    }
+  };
+  int64_t chunk = c.s;
+  if (first && chunk < c.e) {  // loaded while the previous row was counted: its own
+    count_chunk(chunk, *first);  // code path, so no wait here covers later loads
+    chunk += kChunk * kWaveBB;
+  }
+  for (; chunk < c.e; chunk += kChunk * kWaveBB) {
     UIT uk[kChunk];
 #pragma unroll
     for (int k = 0; k < kChunk; ++k)  // clamped, not branched: the row is not empty
       uk[k] = idx[std::min<int64_t>(chunk + k * kWaveBB + lane_id(), c.e - 1)];
+    count_chunk(chunk, uk);
+  }
+}
+
+// The first chunk of a row's indices (up to kChunk x 64) with range-checked
+// buffer loads: lanes past the row, and rows that do not exist (j >= nrows) or
+// are empty, read zero.  Every call issues the same kChunk loads, so the wait for
+// them is exact whatever rows exist.
+template <typename IT, typename OT>
+__device__ __forceinline__ void load_first_chunk(const BBParams<IT, OT>& p, const RowCtx<IT>& c, bool exists,
+                                                 std::make_unsigned_t<IT> (&uk)[kChunk]) {
+  using UIT = std::make_unsigned_t<IT>;
+  // wave-uniform by construction; readfirstlane keeps the descriptor in SGPRs
+  const int n = __builtin_amdgcn_readfirstlane(
+      exists && c.ok ? static_cast<int>(std::min<int64_t>(c.e - c.s, kChunk * kWaveBB)) : 0);
+  const int64_t first = uni(n > 0 ? c.s : 0);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<IT*>(p.indices) + first, 0, n * static_cast<int>(sizeof(IT)), kRsrcWord3);
 #pragma unroll
-    for (int k = 0; k < kChunk; ++k) {
-    const int64_t base = chunk + k * kWaveBB;
-    if (base >= c.e) break;
-    const int64_t i = base + lane_id();
-    const UIT u = uk[k];
-    int64_t b = 0;
-    IT v;
-    bool valid = map_step<FAST, IT>(c, i < c.e, u, p.my_size, p.keep, b, v);
-    if constexpr (REG) {
-      if (valid) atomicAdd(hist + static_cast<uint32_t>(b), 1u);
+  for (int k = 0; k < kChunk; ++k) {
+    const int off = (k * kWaveBB + lane_id()) * static_cast<int>(sizeof(IT));
+    if constexpr (sizeof(IT) == 8) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      uk[k] = static_cast<UIT>((static_cast<uint64_t>(v[1]) << 32) | v[0]);
     } else {
-      uint64_t pending = __builtin_amdgcn_ballot_w64(valid);
-      while (pending) {
-        const int leader = __builtin_ctzll(pending);
-        const int64_t bl = uni(__builtin_amdgcn_readlane(static_cast<int>(b), leader)) & 0xFFFFFFFFll;
-        const bool mine = valid && b == bl;
-        const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
-        const uint32_t k = static_cast<uint32_t>(__builtin_popcountll(m));
-        if (lane_id() == leader) add_count(p.new_lengths + bl * p.L + r, k);
-        pending &= ~m;
-        valid = valid && !mine;
-      }
-    }
+      uk[k] = static_cast<UIT>(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
     }
   }
 }
 
 template <typename IT, typename OT, bool REG>
 __global__ __launch_bounds__(kBBBlock) void bb_count(BBParams<IT, OT> p) {
+  using UIT = std::make_unsigned_t<IT>;
   __shared__ uint32_t lds_hist[kBBBlock / kWaveBB][kWaveBB];
   uint32_t* hist = lds_hist[threadIdx.x >> 6];
   if constexpr (REG) hist[lane_id()] = 0;
@@ -397,19 +434,40 @@ __global__ __launch_bounds__(kBBBlock) void bb_count(BBParams<IT, OT> p) {
     const int64_t rl = g0 + lane_id() * rs;
     const RowCtx<IT> mine = row_ctx_lane(p, rl < r1 ? rl : -1);
     const int nrows = static_cast<int>(std::min<int64_t>(kWaveBB, (r1 - g0 + rs - 1) / rs));
-    for (int j = 0; j < nrows; ++j) {
-    const int64_t r = g0 + j * rs;
-    const RowCtx<IT> c = row_ctx_of(mine, j);
-    if (c.ok) {
-      if (c.fast) count_row<true, REG>(p, c, r, hist);
-      else count_row<false, REG>(p, c, r, hist);
-    }
     if constexpr (REG) {
-      // the wave's LDS operations complete in order: the reads see every add
-      const uint32_t cnt = hist[lane_id()];
-      hist[lane_id()] = 0;
-      if (lane_id() < p.my_size) p.new_lengths[lane_id() * p.L + r] = static_cast<OT>(cnt);
-    }
+      // row j is counted while the first indices of row j + 1 load (two buffers,
+      // no register copies: a copy would wait for the load)
+      auto count_one = [&](int j, const UIT (&buf)[kChunk]) __attribute__((always_inline)) {
+        const int64_t r = g0 + j * rs;
+        const RowCtx<IT> c = row_ctx_of(mine, j);
+        if (c.ok) {
+          if (c.fast) count_row<true, true>(p, c, r, hist, &buf);
+          else count_row<false, true>(p, c, r, hist, &buf);
+        }
+        // the wave's LDS operations complete in order: the reads see every add
+        const uint32_t cnt = hist[lane_id()];
+        hist[lane_id()] = 0;
+        if (lane_id() < p.my_size) p.new_lengths[lane_id() * p.L + r] = static_cast<OT>(cnt);
+      };
+      auto prefetch = [&](int j, UIT (&buf)[kChunk]) __attribute__((always_inline)) {
+        load_first_chunk(p, row_ctx_of(mine, std::min(j, kWaveBB - 1)), j < nrows, buf);
+      };
+      UIT ba[kChunk], bb[kChunk];
+      prefetch(0, ba);
+      for (int j = 0; j < nrows; j += 2) {
+        prefetch(j + 1, bb);
+        count_one(j, ba);
+        if (j + 1 >= nrows) break;
+        prefetch(j + 2, ba);
+        count_one(j + 1, bb);
+      }
+    } else {
+      for (int j = 0; j < nrows; ++j) {
+        const RowCtx<IT> c = row_ctx_of(mine, j);
+        if (!c.ok) continue;
+        if (c.fast) count_row<true, false>(p, c, g0 + j * rs, hist, nullptr);
+        else count_row<false, false>(p, c, g0 + j * rs, hist, nullptr);
+      }
     }
   }
 }
