@@ -346,6 +346,40 @@ __device__ __forceinline__ void accum_row(float (&acc)[Traits<WT>::kEpd], float&
   }
 }
 
+// Two rows at once, unweighted INT8 / INT4: byte k of both rows' words is placed
+// in the two halves of one register (v_perm_b32: {row 1 byte k, 0, row 2 byte k, 0}),
+// so one v_dot2_f32_f16 adds element e of both rows, each times its own fp16 scale
+// (the halves read as q x 2^-24 subnormals, as in accum_row; the products are exact
+// in fp32).  The two biases are summed into bacc by one more dot2 with {1, 1}.
+// Same element order and post-scale as accum_row.
+template <int WT>
+constexpr bool kPairDot = WT == TBE_TY_INT8 || WT == TBE_TY_INT4;
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
+}
+
+template <int WT>
+__device__ __forceinline__ void accum_row_pair(float (&acc)[Traits<WT>::kEpd], float& bacc, uint32_t d1, uint32_t d2,
+                                               uint32_t h1, uint32_t h2) {
+  static_assert(kPairDot<WT>, "INT8 and INT4 rows");
+  const uint32_t s2 = __builtin_amdgcn_perm(h2, h1, 0x05040100u);  // {scale 1, scale 2}
+  const uint32_t b2 = __builtin_amdgcn_perm(h2, h1, 0x07060302u);  // {bias 1, bias 2}
+  bacc = dot2(b2, 0x3C003C00u, bacc);                              // + bias 1 + bias 2
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t x = __builtin_amdgcn_perm(d2, d1, 0x0C000C00u | (static_cast<uint32_t>(4 + k) << 16) | k);
+    if constexpr (WT == TBE_TY_INT8) {
+      acc[k] = dot2(x, s2, acc[k]);
+    } else {  // byte k holds elements 2k (low nibble) and 2k+1 (high nibble, x16)
+      acc[2 * k] = dot2(x & 0x000F000Fu, s2, acc[2 * k]);
+      acc[2 * k + 1] = dot2(x & 0x00F000F0u, s2, acc[2 * k + 1]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- output store
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
@@ -877,6 +911,14 @@ __device__ __forceinline__ void consume_step(const KParams& p, const StepRegs<un
   constexpr int R = kWave >> LG;
   constexpr int U = unroll_for<LG, VW>();
   constexpr int EW = Traits<WT>::kEpd;
+  if constexpr (!WEIGHTED && kPairDot<WT> && VW == 1 && U % 2 == 0) {
+#pragma unroll
+    for (int u = 0; u < U; u += 2) {
+      // wave-uniform; a row past the bag read zero words and a zero header, so it adds 0
+      if (st * R * U + u * R < n) accum_row_pair<WT>(acc, bacc, r.d[u][0], r.d[u + 1][0], r.h[u], r.h[u + 1]);
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (st * R * U + u * R < n) {  // wave-uniform
