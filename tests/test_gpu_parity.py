@@ -300,6 +300,31 @@ def test_edge_cases(pkg, oracle, gpu):
         _check_module(oracle, m, idx, off, psw, f"edge B={B}")
 
 
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+def test_degenerate_sizes(pkg, gpu, idx_dtype):
+    """Calls with no indices at all (B = 0, or every bag empty): the op rejects them
+    as the reference does (A:117, "indices can not be empty tensor."); the C ABI
+    accepts them and leaves every bag zero (A:155) or the output empty."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    specs = [(50, 64, SparseType.INT4), (40, 32, SparseType.INT8), (30, 16, SparseType.FP16)]
+    for pm in (0, 1, 2):
+        sp = specs if pm != 2 else [(50, 32, SparseType.INT4), (40, 32, SparseType.INT8)]
+        m = IntNBitTableBatchedEmbeddingBagsCodegen(sp, device=gpu, pooling_mode=pm,
+                                                    output_dtype=FP16, indices_dtype=idx_dtype)
+        m.fill_random_weights(3)
+        no_idx = torch.zeros(0, dtype=idx_dtype, device=gpu)
+        for B in (0, 5):
+            off = torch.zeros(len(sp) * B + 1, dtype=idx_dtype, device=gpu)
+            _say(f"[gpu] degenerate pm={pm} B={B} {idx_dtype}")
+            with pytest.raises(RuntimeError, match="indices can not be empty tensor"):
+                _op(m, no_idx, off, None)
+            out = _capi_run(pkg, m, no_idx, off, None, 0)
+            torch.cuda.synchronize()
+            rows = 0 if pm == 2 else B
+            assert tuple(out.shape) == (rows, m.total_D if pm != 2 else 32)
+            assert out.numel() == 0 or int(torch.count_nonzero(out)) == 0
+
+
 def test_malformed_offsets_stay_in_bounds(pkg, gpu):
     """Offsets past the index array are clamped to it (no out-of-bounds read)."""
     from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
