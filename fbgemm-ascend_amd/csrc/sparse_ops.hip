@@ -37,7 +37,7 @@ constexpr int kWaveBB = 64;
 constexpr int kChunk = 8;                            // index loads in flight per wave
 constexpr int kRsrcWord3 = 0x00020000;               // raw buffer resource word 3 (gfx9: 32-bit data, no swizzle)
 constexpr int kBBBlock = 256;
-constexpr int kScanItems = 16;                       // elements per thread in the scan
+constexpr int kScanItems = 4;                        // elements per thread in the scan
 constexpr int kScanTile = kBBBlock * kScanItems;     // elements per scan work-group
 
 template <typename IT, typename OT>
@@ -697,14 +697,26 @@ __global__ __launch_bounds__(kBBBlock) void scan_tile_sums(const T* __restrict__
 
 template <typename T>
 __global__ __launch_bounds__(kBBBlock) void scan_sums_exclusive(T* __restrict__ sums, int64_t m) {
+  // one work-group, kSumItems consecutive sums per thread per pass
+  constexpr int kSumItems = 8;
   __shared__ T lds[kBBBlock / kWaveBB];
   T carry = 0;
-  for (int64_t t0 = 0; t0 < m; t0 += kBBBlock) {
-    const int64_t i = t0 + threadIdx.x;
-    const T v = i < m ? sums[i] : T(0);
+  for (int64_t t0 = 0; t0 < m; t0 += static_cast<int64_t>(kBBBlock) * kSumItems) {
+    const int64_t base = t0 + threadIdx.x * static_cast<int64_t>(kSumItems);
+    T v[kSumItems];
+    T s = 0;
+#pragma unroll
+    for (int k = 0; k < kSumItems; ++k) {
+      v[k] = base + k < m ? sums[base + k] : T(0);
+      s += v[k];
+    }
     T total;
-    const T ex = block_exclusive_scan(v, lds, total);
-    if (i < m) sums[i] = carry + ex;
+    T run = carry + block_exclusive_scan(s, lds, total);
+#pragma unroll
+    for (int k = 0; k < kSumItems; ++k) {
+      if (base + k < m) sums[base + k] = run;
+      run += v[k];
+    }
     carry += total;
   }
 }

@@ -202,3 +202,12 @@ def test_bucketize_bucket_past_my_size_dropped(pkg, oracle, gpu, dtype, my_size)
     assert np.array_equal(got[0].cpu().numpy(), want[0])
     assert np.array_equal(got[1].cpu().numpy()[:total], want[1][:total])
     assert np.array_equal(got[2].cpu().numpy()[:total], want[2][:total])
+
+
+@pytest.mark.parametrize("my_size", [64, 100])
+def test_bucketize_many_segments(pkg, oracle, gpu, my_size):
+    # my_size * rows above 2^21 segments: the device scan of new_lengths takes
+    # more than one pass over its tile sums
+    from _bucketize_cases import Case
+    case = Case(f"segments_my{my_size}", 8, 5000, 0, 3, 4, 8, my_size, np.int64)
+    _check(oracle, gpu, case, 41, weights=True, sequence=True)
