@@ -516,8 +516,34 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     for (int i = 0; i < used; ++i)
       if (hipStreamWaitEvent(gs->st[i], gs->fork, 0) != hipSuccess) return fail(TBE_ERR_LAUNCH, "fork wait failed");
   }
-  for (int gi = 0; gi < plan.num_groups; ++gi) {
-    const hipStream_t gstream = gs ? gs->st[gi % used] : s;
+  // Groups in decreasing estimated cost, each on the group stream with the least
+  // cost so far (longest-processing-time-first), so the streams finish together.
+  // Cost ~ tables x (lane words of a row + a per-bag constant); bag lengths are on
+  // the device and are not read.  Groups write disjoint output columns, so the
+  // assignment does not change results.
+  int gorder[TBE_MAX_GROUPS];
+  int gsid[TBE_MAX_GROUPS];
+  {
+    int64_t cost[TBE_MAX_GROUPS];
+    for (int gi = 0; gi < plan.num_groups; ++gi) {
+      const TbePlanGroup& g = plan.groups[gi];
+      cost[gi] = static_cast<int64_t>(g.count) * ((int64_t(4) << std::max(0, std::min(g.log2_lanes, 6))) *
+                                                     std::max(1, g.col_tiles) + 64);
+      gorder[gi] = gi;
+    }
+    std::stable_sort(gorder, gorder + plan.num_groups, [&](int x, int y) { return cost[x] > cost[y]; });
+    int64_t load[kGroupStreams] = {};
+    for (int k = 0; k < plan.num_groups; ++k) {
+      int best = 0;
+      for (int i = 1; i < used; ++i)
+        if (load[i] < load[best]) best = i;
+      gsid[gorder[k]] = best;
+      load[best] += cost[gorder[k]];
+    }
+  }
+  for (int k = 0; k < plan.num_groups; ++k) {
+    const int gi = gorder[k];
+    const hipStream_t gstream = gs ? gs->st[gsid[gi]] : s;
     const TbePlanGroup& g = plan.groups[gi];
     if (g.count <= 0 || g.first < 0 || g.first + g.count > a->T || g.col_tiles < 1 || g.col_tiles > 255)
       return fail(TBE_ERR_INVALID_ARG, "bad plan group %d", gi);
