@@ -101,7 +101,7 @@ load_library()
 
 from . import capi  # noqa: E402,F401
 from .sparse_types import PoolingMode, SparseType  # noqa: E402,F401
-from .tbe_module import IntNBitTableBatchedEmbeddingBagsCodegen  # noqa: E402,F401
+from .tbe_module import IntNBitTableBatchedEmbeddingBagsCodegen, fp8_code_values, fp8_quantize  # noqa: E402,F401
 from .permute_pooled_embedding_modules import PermutePooledEmbeddings  # noqa: E402,F401
 
 

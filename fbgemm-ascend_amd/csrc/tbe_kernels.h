@@ -114,6 +114,7 @@ struct KParams {
   int32_t xcd;
   int32_t ranges;         // bag ranges per table (stream kernel)
   int32_t bags_per_wave;  // bags of one range
+  int32_t zero_gaps;      // nobag: this launch zeroes output rows outside every table's segment
   FastDiv div_B;
   FastDiv div_tiles;
   FastDiv div_ranges;
@@ -1417,6 +1418,24 @@ __device__ __forceinline__ void nobag_segment(const KParams& p, const TbeTableDe
   }
 }
 
+// Output rows of positions that no table's segment covers (before offsets[0], or
+// from offsets[T*B] on, e.g. when len(offsets)-1 is not a multiple of T) are
+// zero, as the reference's zero-initialised output leaves them (A:135).  One
+// launch of a forward (p.zero_gaps) writes them.
+__device__ __forceinline__ void nobag_zero_gaps(const KParams& p, int64_t i0, int64_t i1) {
+  const int64_t first = load_offset(p, 0);
+  const int64_t last = load_offset(p, static_cast<int64_t>(p.T) * p.B);
+  if (i0 >= first && i1 <= last) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int64_t i = i0; i < i1; ++i) {
+    if (i >= first && i < last) continue;
+    for (int64_t c = lane; c < p.out_stride; c += kWave) {
+      if (p.out_ty == TBE_TY_FP32) static_cast<float*>(p.out)[i * p.out_stride + c] = 0.f;
+      else static_cast<uint16_t*>(p.out)[i * p.out_stride + c] = 0;
+    }
+  }
+}
+
 template <int WT, int LG, typename IndexT>
 __global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
   const int wv = uniform(threadIdx.x >> 6);
@@ -1424,6 +1443,7 @@ __global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
   if (item >= p.num_items) return;
   const int64_t i0 = item * kWave;
   const int64_t i1 = min(i0 + kWave, p.num_indices);
+  if (p.zero_gaps) nobag_zero_gaps(p, i0, i1);
   // last table whose first index is <= i0 (N:57-78 walks tables by offset_per_key)
   int lo = 0, hi = p.T - 1;
   while (lo < hi) {

@@ -88,6 +88,7 @@ __global__ __launch_bounds__(kBlock) void nobag_kernel(KParams p) {
   if (item >= p.num_items) return;
   const int64_t i0 = item * kWave;
   const int64_t i1 = min(i0 + kWave, p.num_indices);
+  if (p.zero_gaps) nobag_zero_gaps(p, i0, i1);
   // last table whose first index is <= i0 (N:57-78 walks tables by offset_per_key)
   int lo = 0, hi = p.T - 1;
   while (lo < hi) {
@@ -253,15 +254,21 @@ int resident_blocks(KernelFn fn) {
 // Streams that run a forward's table groups side by side: the groups write
 // disjoint output columns, and a persistent kernel's tail (its last waves)
 // leaves most of the GPU idle while the next group's kernel would wait behind
-// it on one stream.  Created once per device, default priority, ordered
-// against the caller's stream with events (fork before, join after), so the
-// call stays asynchronous.
+// it on one stream.  One set per (device, caller stream), default priority,
+// ordered against the caller's stream with events (fork before, join after), so
+// the call stays asynchronous, calls on independent caller streams stay
+// independent, and a caller stream under graph capture brings only its own
+// side streams into the capture.  Sets are kept until the process ends; past
+// kMaxStreamSets caller streams on one device, further streams run their
+// groups serially on the caller's stream.
 // Two streams measured best on config 3 (14 groups): 0.854 ms serial, 0.782 ms
 // with 2, 0.814 ms with 4, 0.810 ms with 8.
 constexpr int kGroupStreams = 2;
+constexpr int kMaxStreamSets = 32;
 
 struct GroupStreams {
   int dev = -1;
+  hipStream_t caller = nullptr;
   bool ok = false;
   std::mutex mu;
   hipStream_t st[kGroupStreams] = {};
@@ -269,16 +276,22 @@ struct GroupStreams {
   hipEvent_t join[kGroupStreams] = {};
 };
 
-GroupStreams* group_streams() {
+GroupStreams* group_streams(hipStream_t caller) {
   static std::mutex mu;
   static std::vector<GroupStreams*> all;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> g(mu);
-  for (GroupStreams* e : all)
-    if (e->dev == dev) return e->ok ? e : nullptr;
+  int on_dev = 0;
+  for (GroupStreams* e : all) {
+    if (e->dev != dev) continue;
+    if (e->caller == caller) return e->ok ? e : nullptr;
+    ++on_dev;
+  }
+  if (on_dev >= kMaxStreamSets) return nullptr;
   GroupStreams* e = new GroupStreams();  // kept until the process ends
   e->dev = dev;
+  e->caller = caller;
   bool ok = hipEventCreateWithFlags(&e->fork, hipEventDisableTiming) == hipSuccess;
   for (int i = 0; ok && i < kGroupStreams; ++i)
     ok = hipStreamCreateWithFlags(&e->st[i], hipStreamNonBlocking) == hipSuccess &&
@@ -481,7 +494,9 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     // one launch per table group: 32-bit groups take their specialised kernel,
     // which skips other tables' segments; tables beyond 32-bit addressing take
     // the generic kernel
+    // the first launch also zeroes the rows of positions outside every segment
     bool generic = false;
+    p.zero_gaps = 1;
     for (int gi = 0; gi < plan.num_groups; ++gi) {
       const TbePlanGroup& g = plan.groups[gi];
       if (!g.offset32) {
@@ -491,6 +506,7 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
       const hipError_t err = launch(nobag_kernel_group(g, p.index64 != 0), p,
                                     (chunks + kWavesPerBlock - 1) / kWavesPerBlock, false, s);
       if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+      p.zero_gaps = 0;
     }
     if (generic) {
       const hipError_t err = launch(nobag_kernel, p, (chunks + kWavesPerBlock - 1) / kWavesPerBlock, false, s);
@@ -502,19 +518,24 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
   if (!a->table_order) return fail(TBE_ERR_INVALID_ARG, "null table_order");
   const TbePlanSummary& plan = *a->plan;
   if (plan.num_groups < 1 || plan.num_groups > TBE_MAX_GROUPS) return fail(TBE_ERR_INVALID_ARG, "bad plan");
+  for (int gi = 0; gi < plan.num_groups; ++gi) {
+    const TbePlanGroup& g = plan.groups[gi];
+    if (g.count <= 0 || g.first < 0 || g.first + g.count > a->T || g.col_tiles < 1 || g.col_tiles > 255)
+      return fail(TBE_ERR_INVALID_ARG, "bad plan group %d", gi);
+  }
   const bool weighted = a->indice_weights != nullptr;
   // the per-group kernels keep index positions in 32 bits
   const bool wide = a->num_indices > 0x7FFFFFFF;
   // several groups: launch them on the group streams, between a fork and a join
-  GroupStreams* gs = (plan.num_groups > 1 && !(a->flags & TBE_FLAG_SERIAL_GROUPS)) ? group_streams() : nullptr;
+  GroupStreams* gs = (plan.num_groups > 1 && !(a->flags & TBE_FLAG_SERIAL_GROUPS)) ? group_streams(s) : nullptr;
   std::unique_lock<std::mutex> gs_lock;
   int used = 0;
   if (gs) {
     gs_lock = std::unique_lock<std::mutex>(gs->mu);
-    used = std::min(kGroupStreams, plan.num_groups);
     if (hipEventRecord(gs->fork, s) != hipSuccess) return fail(TBE_ERR_LAUNCH, "fork event failed");
-    for (int i = 0; i < used; ++i)
-      if (hipStreamWaitEvent(gs->st[i], gs->fork, 0) != hipSuccess) return fail(TBE_ERR_LAUNCH, "fork wait failed");
+    for (int i = 0; i < std::min(kGroupStreams, plan.num_groups); ++i, ++used)
+      if (hipStreamWaitEvent(gs->st[i], gs->fork, 0) != hipSuccess) break;
+    if (used == 0) return fail(TBE_ERR_LAUNCH, "fork wait failed");
   }
   // Groups in decreasing estimated cost, each on the group stream with the least
   // cost so far (longest-processing-time-first), so the streams finish together.
@@ -541,17 +562,15 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
       load[best] += cost[gorder[k]];
     }
   }
-  for (int k = 0; k < plan.num_groups; ++k) {
+  hipError_t err = hipSuccess;
+  for (int k = 0; k < plan.num_groups && err == hipSuccess; ++k) {
     const int gi = gorder[k];
     const hipStream_t gstream = gs ? gs->st[gsid[gi]] : s;
     const TbePlanGroup& g = plan.groups[gi];
-    if (g.count <= 0 || g.first < 0 || g.first + g.count > a->T || g.col_tiles < 1 || g.col_tiles > 255)
-      return fail(TBE_ERR_INVALID_ARG, "bad plan group %d", gi);
     p.group_first = g.first;
     p.group_count = g.count;
     p.col_tiles = g.col_tiles;
     p.div_tiles = make_fastdiv(static_cast<uint32_t>(g.col_tiles));
-    hipError_t err;
     // row streams pay off on large groups (measured: 200 tables x 32768 bags, 25 %
     // faster); the per-bag kernel is as fast or faster below about a million bags
     const int64_t group_bags = static_cast<int64_t>(g.count) * a->B * g.col_tiles;
@@ -575,13 +594,15 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
       err = launch(pooled_kernel_for(g, p.index64 != 0, weighted, wide, wide_words), p,
                    (items + kWavesPerBlock - 1) / kWavesPerBlock, true, gstream);
     }
-    if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }
-  if (gs) {
-    for (int i = 0; i < used; ++i)
-      if (hipEventRecord(gs->join[i], gs->st[i]) != hipSuccess || hipStreamWaitEvent(s, gs->join[i], 0) != hipSuccess)
-        return fail(TBE_ERR_LAUNCH, "join of the group streams failed");
-  }
+  // join even after a failed launch, so the caller's stream still waits for the
+  // groups already queued before it frees or reuses the output
+  bool joined = true;
+  for (int i = 0; i < used; ++i)
+    if (hipEventRecord(gs->join[i], gs->st[i]) != hipSuccess || hipStreamWaitEvent(s, gs->join[i], 0) != hipSuccess)
+      joined = false;
+  if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  if (!joined) return fail(TBE_ERR_LAUNCH, "join of the group streams failed");
   return TBE_OK;
 }
 

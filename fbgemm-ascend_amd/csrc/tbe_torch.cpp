@@ -11,7 +11,7 @@
 //
 // Table metadata (weights_offsets, weights_tys, D_offsets) is planned once on
 // the host and the device copy of the plan is cached, keyed on the tensors'
-// storage and version counters: TorchRec-style modules pass the same buffers
+// addresses and version counters (each entry keeps those tensors alive): TorchRec-style modules pass the same buffers
 // every call, so after the first call no host synchronisation happens.
 #include <ATen/ATen.h>
 #include <ATen/DeviceGuard.h>
@@ -76,13 +76,13 @@ class PlanCache {
            const Tensor& D_offsets, const at::Device& dev) {
     std::lock_guard<std::mutex> g(mu_);
     for (auto it = entries_.begin(); it != entries_.end(); ++it) {
-      if (it->first == key) {
+      if (it->key == key) {
         entries_.splice(entries_.begin(), entries_, it);
-        return entries_.front().second;
+        return entries_.front().plan;
       }
     }
     Plan p = build(key, weights_offsets, weights_tys, D_offsets, dev);
-    entries_.emplace_front(key, p);
+    entries_.push_front(Entry{key, p, weights_offsets, weights_tys, D_offsets});
     if (entries_.size() > kMaxEntries) entries_.pop_back();
     return p;
   }
@@ -119,8 +119,17 @@ class PlanCache {
     return p;
   }
 
+  // An entry holds the keyed metadata tensors, so their storage (and with it the
+  // addresses in the key) cannot be freed and handed to other tensors while the
+  // entry lives: an address match therefore means the same tensor, and the
+  // version counter catches in-place writes to it.
+  struct Entry {
+    PlanKey key;
+    Plan plan;
+    Tensor weights_offsets, weights_tys, D_offsets;
+  };
   std::mutex mu_;
-  std::list<std::pair<PlanKey, Plan>> entries_;
+  std::list<Entry> entries_;
 };
 
 PlanCache& plan_cache() {

@@ -21,6 +21,44 @@ import torch
 from .sparse_types import PoolingMode, SparseType, row_stride
 
 
+def fp8_code_values(exponent_bits: int, exponent_bias: int) -> torch.Tensor:
+    """fp32 values of the 128 non-negative FP8 codes 0x00..0x7F, increasing.
+
+    Format of c310/op_kernel/common.h:120-167: a code is [sign][exponent_bits
+    exponent bits E][m = 7 - exponent_bits mantissa bits M]; E > 0 is the normal
+    value 2^(E - bias) * (1 + M / 2^m), E = 0 the subnormal 2^(1 - bias) * M / 2^m.
+    No Inf / NaN codes.
+    """
+    if not (1 <= exponent_bits <= 7 and 0 <= exponent_bias <= 120):
+        raise ValueError(f"bad FP8 parameters ({exponent_bits}, {exponent_bias})")
+    m = 7 - exponent_bits
+    code = torch.arange(128, dtype=torch.float64)
+    E = torch.div(code, 1 << m, rounding_mode="floor")
+    M = code - E * (1 << m)
+    normal = torch.exp2(E - exponent_bias) * (1 + M / (1 << m))
+    sub = 2.0 ** (1 - exponent_bias) * M / (1 << m)
+    return torch.where(E > 0, normal, sub).to(torch.float32)
+
+
+def fp8_quantize(w: torch.Tensor, exponent_bits: int, exponent_bias: int) -> torch.Tensor:
+    """Nearest FP8 code of every element (uint8, same shape).  Ties go to the even
+    code (even mantissa); magnitudes above the largest code saturate to it; the
+    sign bit follows the sign of w (-0.0 keeps it)."""
+    vals = fp8_code_values(exponent_bits, exponent_bias).to(w.device, torch.float64)
+    x = w.to(torch.float64)
+    a = x.abs()
+    hi = torch.searchsorted(vals, a).clamp(1, 127)  # vals[hi-1] < a <= vals[hi] inside the range
+    lo = hi - 1
+    dlo = a - vals[lo]
+    dhi = vals[hi] - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = torch.where(pick_hi, hi, lo)
+    code = torch.where(a >= vals[127], torch.full_like(code, 127), code)
+    code = torch.where(a <= vals[0], torch.zeros_like(code), code)
+    sign = torch.signbit(x).to(torch.int64) << 7
+    return (code | sign).to(torch.uint8)
+
+
 def _spec_fields(spec) -> Tuple[int, int, SparseType]:
     # accepts (E, D, ty) or fbgemm's (name, E, D, ty, location)
     if len(spec) == 3:
@@ -130,7 +168,10 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
     @torch.no_grad()
     def load_float_weights(self, t: int, weight: torch.Tensor) -> None:
         """Quantize a float [E, D] table into table t (row-wise min/max for INT types:
-        scale = (max-min)/(2^bits-1), bias = min, q = round((w-bias)/scale))."""
+        scale = (max-min)/(2^bits-1), bias = min, q = round((w-bias)/scale), with scale
+        and bias stored as fp16; FP8: the nearest code under the module's
+        (fp8_exponent_bits, fp8_exponent_bias), see fp8_quantize; FP16/BF16/FP32: a
+        cast)."""
         E, D, ty = self.specs[t]
         w = weight.to(self.device_, torch.float32)
         if tuple(w.shape) != (E, D):
@@ -142,7 +183,9 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
             payload.copy_(w.to(fdt).view(torch.uint8).view(E, -1))
             return
         if ty == SparseType.FP8:
-            raise NotImplementedError("FP8 quantization from float is not provided; write codes directly")
+            codes = fp8_quantize(w, self.fp8_exponent_bits, self.fp8_exponent_bias)
+            payload.copy_(codes)
+            return
         bits = ty.bit_rate()
         lo = w.min(dim=1).values
         hi = w.max(dim=1).values

@@ -130,7 +130,9 @@ typedef struct TbePlanSummary {
  * output[num_indices, output_stride] (output_stride = max_D).
  * Every output element inside a table's column range is written, including
  * the zeros of empty bags, so the caller need not pre-clear the output when
- * TbePlanSummary.covers_output is 1.
+ * TbePlanSummary.covers_output is 1.  Nobag writes every one of the
+ * num_indices output rows: rows of positions outside [offsets[0], offsets[T*B])
+ * are zero.
  */
 typedef struct TbeNbitArgs {
   const uint8_t* dev_weights;      /* packed rows of all tables                 */

@@ -1,0 +1,366 @@
+"""GPU parity of the paths the random matrices do not reach:
+
+* tables whose rows span more than 4 GiB (64-bit addressing: the generic pooled
+  kernel and the generic nobag kernel), and calls with more than 2^31 indices;
+* FP8 rows under exponent-bit / bias pairs other than (4, 7), so both FP8 decodes
+  run (fp16 placement for exponent_bits <= 4, shift-and-multiply above);
+* the plan cache under freed and reallocated table metadata;
+* nobag output rows outside every table's segment;
+* the module packer: float tables -> load_float_weights -> the HIP op, against the
+  dequantised table (oracle) and against the float table within the quantisation
+  bound.
+
+Reference: c310/op_kernel/common.h:120-167 (FP8), int_nbit_split_embedding_pooling_kernel.h:235-278
+(row addressing), test_int_nbit_split_embedding_codegen_lookup_function.py:121-156 (packer use).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from _parity import assert_bag_parity, compact_problem, run_oracle
+from test_gpu_parity import OUT_TORCH, _check_module, _random_case
+
+pytestmark = pytest.mark.gpu
+
+FP32, FP16, INT8, INT4, INT2, BF16, FP8 = 0, 1, 2, 3, 4, 5, 6
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _free_gib():
+    free, _ = torch.cuda.mem_get_info()
+    return free / 2 ** 30
+
+
+# ----------------------------------------------------------------- tables beyond 32-bit addressing
+
+BIG_ROWS = 60_000_000  # INT4 D=128: 80-byte rows, 4.8 GB, past the 0xFFFE0000-byte limit
+
+
+@pytest.fixture(scope="module")
+def big_tables(gpu):
+    """One 4.8 GB INT4 table next to a small INT8 table (same D, so nobag applies)."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    if _free_gib() < 16:
+        pytest.skip("needs ~6 GiB of free HBM")
+    specs = [(BIG_ROWS, 128, SparseType.INT4), (1000, 128, SparseType.INT8)]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device=gpu)
+    m.fill_random_weights(60)
+    yield m
+    del m
+    torch.cuda.empty_cache()
+
+
+def _big_inputs(gpu, idx_dtype, B=96, L=40, seed=5):
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    lens = torch.randint(0, 2 * L, (2 * B,), device=gpu, generator=g)
+    lens[::11] = 0
+    off = torch.zeros(2 * B + 1, dtype=torch.int64, device=gpu)
+    torch.cumsum(lens, 0, out=off[1:])
+    n0, N = int(off[B]), int(off[-1])
+    big = torch.randint(BIG_ROWS - 50000, BIG_ROWS + 2, (n0,), device=gpu, generator=g)  # last rows + 2 past the end
+    big[::5] = torch.randint(0, BIG_ROWS, (big[::5].numel(),), device=gpu, generator=g)
+    small = torch.randint(0, 1000, (N - n0,), device=gpu, generator=g)
+    idx = torch.cat([big, small]).to(idx_dtype)
+    psw = torch.rand(N, device=gpu, generator=g)
+    return idx, off.to(idx_dtype), psw
+
+
+def test_big_table_plan_is_64bit(pkg, big_tables):
+    m = big_tables
+    plan = pkg.capi.plan(m.weights_offsets.cpu().numpy(), m.weights_tys.cpu().numpy(), m.D_offsets.cpu().numpy(),
+                         m.weights_dev.numel())
+    descs = plan[0]
+    assert not (descs[0].flags & pkg.capi.TBE_TABLE_OFFSET32)
+    assert descs[1].flags & pkg.capi.TBE_TABLE_OFFSET32
+
+
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("pm,weighted,out_ty", [(0, False, FP16), (1, True, FP32), (0, True, BF16)])
+def test_big_table_pooled(pkg, oracle, gpu, big_tables, idx_dtype, pm, weighted, out_ty):
+    """pooled_wide_kernel on a 4.8 GB table (its last rows, two indices past the end)."""
+    m = big_tables
+    m.pooling_mode = pkg.PoolingMode(pm)
+    m.output_dtype = out_ty
+    idx, off, psw = _big_inputs(gpu, idx_dtype)
+    _check_module(oracle, m, idx, off, psw if weighted else None,
+                  f"4.8 GB table pm={pm} w={weighted} {idx_dtype} out={out_ty}")
+
+
+@pytest.mark.parametrize("out_ty", [FP16, FP32])
+def test_big_table_nobag(pkg, oracle, gpu, big_tables, out_ty):
+    """The generic nobag kernel (64-bit table) next to the specialised one (small table)."""
+    m = big_tables
+    m.pooling_mode = pkg.PoolingMode(2)
+    m.output_dtype = out_ty
+    idx, off, _ = _big_inputs(gpu, torch.int32)
+    _check_module(oracle, m, idx, off, None, f"4.8 GB table nobag out={out_ty}")
+
+
+def test_more_than_2pow31_indices(pkg, gpu):
+    """A call with 2^31 + 4096 indices (positions past 32 bits take the generic
+    kernel).  Exact known answer: an FP32 D=4 table whose element c of row r is
+    bit c of r, so every bag sum is an integer count below 2^24 (exact in fp32 in
+    any order); counts are taken with torch.bincount per bag."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    if _free_gib() < 40:
+        pytest.skip("needs ~30 GiB of free HBM")
+    E, D, B = 1000, 4, 2048
+    N = (1 << 31) + 4096
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(E, D, SparseType.FP32)], device=gpu, output_dtype=FP32)
+    r = torch.arange(E, device=gpu)
+    table = torch.stack([((r >> c) & 1).float() for c in range(D)], 1)
+    m.load_float_weights(0, table)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(31)
+    idx = torch.randint(0, E, (N,), device=gpu, generator=g, dtype=torch.int32)
+    cuts = torch.sort(torch.randint(0, N + 1, (B - 1,), device=gpu, generator=g)).values
+    off = torch.cat([torch.zeros(1, dtype=torch.int64, device=gpu), cuts,
+                     torch.full((1,), N, dtype=torch.int64, device=gpu)]).to(torch.int32)
+    _say(f"[gpu] 2^31+ indices: N={N} B={B}")
+    for pm in (0, 1):
+        m.pooling_mode = pkg.PoolingMode(pm)
+        out = m(idx, off, None)
+        torch.cuda.synchronize()
+        offs = off.to(torch.int64).cpu().tolist()
+        want = torch.zeros(B, D, dtype=torch.float64)
+        for b in range(B):
+            cnt = torch.bincount(idx[offs[b]:offs[b + 1]].to(torch.int64), minlength=E).double().cpu()
+            want[b] = cnt @ table.double().cpu()
+        if pm == 1:
+            L = torch.tensor([offs[b + 1] - offs[b] for b in range(B)], dtype=torch.float32)
+            want = (want.float() * (1.0 / torch.clamp(L, min=1.0))[:, None]).double()  # float(1)/float(L), P:355
+        assert torch.equal(out.cpu().double(), want), f"pm={pm}"
+    del idx, off, m
+    torch.cuda.empty_cache()
+
+
+# ----------------------------------------------------------------- FP8 exponent widths and biases
+
+FP8_PARAMS = [(5, 15), (3, 3), (4, 8), (2, 1), (6, 31), (1, 0), (7, 60)]
+
+
+def _fp8_case(pkg, gpu, seed, T, eb, bias, pm, weighted, idx_dtype, out_ty):
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    rs = np.random.RandomState(seed)
+    D = 4 * int(rs.randint(1, 300))
+    tables = [(int(rs.randint(1, 5000)), D if pm == 2 else 4 * int(rs.randint(1, 300))) for _ in range(T)]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(E, d, SparseType.FP8) for E, d in tables], device=gpu,
+                                                pooling_mode=pm, output_dtype=out_ty, indices_dtype=idx_dtype,
+                                                fp8_exponent_bits=eb, fp8_exponent_bias=bias)
+    m.fill_random_weights(seed)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    B = 37
+    lens = torch.randint(0, 90, (T * B,), device=gpu, generator=g)
+    off = torch.zeros(T * B + 1, dtype=torch.int64, device=gpu)
+    torch.cumsum(lens, 0, out=off[1:])
+    offs = off.cpu()
+    idx = torch.cat([torch.randint(0, E, (int(offs[(t + 1) * B] - offs[t * B]),), device=gpu, generator=g)
+                     for t, (E, _) in enumerate(tables)]).to(idx_dtype)
+    psw = torch.rand(idx.numel(), device=gpu, generator=g) if weighted else None
+    return m, idx, off.to(idx_dtype), psw
+
+
+def _fp8_params():
+    out = []
+    for eb, bias in FP8_PARAMS:
+        # fp16 / bf16 outputs only where every sum stays inside their range
+        outs = (FP32, FP16, BF16) if eb <= 4 else (FP32, BF16)
+        for pm, weighted in ((0, False), (1, True), (2, False)):
+            for idx_dtype in (torch.int32, torch.int64):
+                for out_ty in outs:
+                    if pm == 2 and idx_dtype != torch.int32:
+                        continue
+                    out.append((eb, bias, pm, weighted, idx_dtype, out_ty))
+    return out
+
+
+@pytest.mark.parametrize("kernel", ["default", "stream"])
+@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("eb,bias,pm,weighted,idx_dtype,out_ty", _fp8_params())
+def test_fp8_exponent_params(pkg, oracle, gpu, T, eb, bias, pm, weighted, idx_dtype, out_ty, kernel):
+    if kernel == "stream" and pm == 2:
+        pytest.skip("nobag has one kernel per group")
+    seed = (eb * 131 + bias * 7 + pm * 3 + T) & 0xFFFF
+    m, idx, off, psw = _fp8_case(pkg, gpu, seed, T, eb, bias, pm, weighted, idx_dtype, out_ty)
+    flags = pkg.capi.TBE_FLAG_FORCE_STREAM if kernel == "stream" else None
+    _check_module(oracle, m, idx, off, psw, f"fp8 ({eb},{bias}) T={T} pm={pm} w={weighted} {idx_dtype} out={out_ty}",
+                  flags=flags)
+
+
+# ----------------------------------------------------------------- plan cache
+
+def test_plan_cache_survives_reallocated_metadata(pkg, oracle, gpu):
+    """Modules built and freed in turn, with the same table count and weight bytes but
+    a different table order (so different types, D and offsets): each call must use
+    its own module's layout even when the allocator hands out the freed addresses."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    a = [(1000, 128, SparseType.INT4), (2000, 64, SparseType.INT8)]  # 80 + 80 byte rows
+    b = [(2000, 64, SparseType.INT8), (1000, 128, SparseType.INT4)]
+    c = [(1000, 128, SparseType.INT8), (2000, 32, SparseType.FP16)]  # 144 + 64 byte rows, other total
+    for it in range(6):
+        specs = (a, b, c)[it % 3]
+        m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device=gpu, output_dtype=FP32)
+        m.fill_random_weights(it)
+        g = torch.Generator(device=gpu)
+        g.manual_seed(it)
+        B, L = 16, 9
+        off = torch.arange(0, 2 * B * L + 1, L, dtype=torch.int32, device=gpu)
+        idx = torch.cat([torch.randint(0, E, (B * L,), device=gpu, generator=g) for E, _, _ in specs]).to(torch.int32)
+        _check_module(oracle, m, idx, off, None, f"plan cache round {it}")
+        del m, idx, off
+
+
+def test_plan_cache_sees_in_place_metadata_writes(pkg, oracle, gpu):
+    """An in-place write to weights_tys (same tensor, same address) replans."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(500, 64, SparseType.FP16), (500, 64, SparseType.BF16)],
+                                                device=gpu, output_dtype=FP32)
+    m.fill_random_weights(3)
+    idx = torch.randint(0, 500, (80,), device=gpu, dtype=torch.int32)
+    off = torch.arange(0, 81, 10, dtype=torch.int32, device=gpu)
+    first = m(idx, off, None)
+    m.weights_tys[0] = int(SparseType.BF16)  # rows now read as bf16
+    m.specs[0] = (500, 64, SparseType.BF16)
+    second = m(idx, off, None)
+    torch.cuda.synchronize()
+    assert not torch.equal(first[:, :64], second[:, :64])
+    _check_module(oracle, m, idx, off, None, "in-place weights_tys")
+
+
+# ----------------------------------------------------------------- nobag rows outside every segment
+
+@pytest.mark.parametrize("out_ty", [FP32, FP16])
+@pytest.mark.parametrize("case", ["leading", "trailing", "ragged"])
+def test_nobag_rows_outside_segments_are_zero(pkg, oracle, gpu, out_ty, case):
+    """offsets[0] > 0, indices past offsets[T*B], and len(offsets)-1 not a multiple of
+    T: those output rows are zero (the reference allocates the output with zeros,
+    A:135).  The output memory is poisoned beforehand so stale values would show."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    specs = [(300, 16, SparseType.FP32), (200, 16, SparseType.INT8), (100, 16, SparseType.FP16)]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device=gpu, pooling_mode=2, output_dtype=out_ty)
+    m.fill_random_weights(9)
+    T, B = 3, 5
+    lens = [3, 0, 4, 1, 2] * T
+    base = {"leading": 70, "trailing": 0, "ragged": 0}[case]
+    off = [base] + list(base + np.cumsum(lens))
+    if case == "ragged":
+        off = off + [off[-1] + 6, off[-1] + 9]  # two extra bags: (len(offsets) - 1) % T != 0
+    n_extra = {"leading": 20, "trailing": 150, "ragged": 0}[case]
+    N = off[-1] + n_extra
+    rs = np.random.RandomState(len(case))
+    idx_np = rs.randint(0, 100, N).astype(np.int32)
+    for _ in range(3):
+        junk = torch.full((N * 16 * 4,), float("nan"), device=gpu)
+        del junk
+    off_np = np.asarray(off, np.int32)
+    out = m(torch.from_numpy(idx_np).to(gpu), torch.from_numpy(off_np).to(gpu), None)
+    torch.cuda.synchronize()
+    ref, _ = oracle.forward(m.weights_dev.cpu().numpy(), m.weights_offsets.cpu().numpy(),
+                            m.weights_tys.cpu().numpy(), m.D_offsets.cpu().numpy(), idx_np, off_np, 2, None,
+                            out_ty)
+    got = out.cpu()
+    assert tuple(got.shape) == ref.shape == (N, 16)
+    bits = got.numpy() if out_ty == FP32 else got.view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(bits, ref)  # fp16 output: the oracle returns the bit patterns
+    first, last = off[0], off[T * ((len(off) - 1) // T)]
+    outside = np.r_[0:first, last:N]
+    assert not got[outside].float().any()
+
+
+# ----------------------------------------------------------------- packer: float -> quantised -> op
+
+def _dequantised_table(oracle, m, t):
+    """Float rows of table t as the oracle decodes them (nobag over every row)."""
+    E, D, ty = m.specs[t]
+    rows = m.table_rows(t).cpu().numpy().reshape(-1)
+    out, _ = oracle.forward(rows, np.zeros(1, np.int64), np.array([int(ty)], np.uint8),
+                            np.array([0, D], np.int32), np.arange(E, dtype=np.int32),
+                            np.array([0, E], np.int32), 2, None, FP32,
+                            fp8_exponent_bits=m.fp8_exponent_bits, fp8_exponent_bias=m.fp8_exponent_bias)
+    return out.astype(np.float64)
+
+
+def _quant_bound(m, t, w):
+    """Per-row bound of |dequantised - float| after load_float_weights."""
+    E, D, ty = m.specs[t]
+    w = w.double()
+    if ty == FP8:
+        from fbgemm_ascend_amd import fp8_code_values
+        vals = fp8_code_values(m.fp8_exponent_bits, m.fp8_exponent_bias).double()
+        k = torch.searchsorted(vals, w.abs()).clamp(1, 127)
+        return ((vals[k] - vals[k - 1]) / 2).max(1).values
+    bits = {INT8: 8, INT4: 4, INT2: 2}[int(ty)]
+    lo, hi = w.min(1).values, w.max(1).values
+    step = (hi - lo) / ((1 << bits) - 1)
+    # half a step, plus the fp16 rounding of scale (times the largest code) and of bias
+    return step / 2 + ((1 << bits) - 1) * step.abs() * 2.0 ** -11 + lo.abs() * 2.0 ** -11 + 1e-7
+
+
+@pytest.mark.parametrize("ty", [INT8, INT4, INT2, FP8])
+@pytest.mark.parametrize("pm,weighted", [(0, False), (1, True)])
+def test_packer_float_to_op(pkg, oracle, gpu, ty, pm, weighted):
+    """T:121-156 builds a module, fills its rows and runs the op.  Here: float tables
+    -> load_float_weights -> the HIP op, checked (1) against F.embedding_bag over the
+    oracle's dequantised tables (fp32 tolerance of the parity tests) and (2) against
+    F.embedding_bag over the float tables within sum_i |w_i| * (quantisation bound)."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    specs = [(3000, 128, SparseType(ty)), (1500, 64, SparseType(ty)), (700, 32, SparseType(ty))]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device=gpu, pooling_mode=pm, output_dtype=FP32,
+                                                fp8_exponent_bits=4 if ty == FP8 else None,
+                                                fp8_exponent_bias=7 if ty == FP8 else None)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(ty * 10 + pm)
+    floats = []
+    for t, (E, D, _) in enumerate(specs):
+        w = torch.randn(E, D, device=gpu, generator=g) * 0.5
+        m.load_float_weights(t, w)
+        floats.append(w)
+    B = 64
+    lens = torch.randint(0, 60, (len(specs) * B,), device=gpu, generator=g)
+    off = torch.zeros(len(specs) * B + 1, dtype=torch.int64, device=gpu)
+    torch.cumsum(lens, 0, out=off[1:])
+    offs = off.cpu()
+    idx = torch.cat([torch.randint(0, E, (int(offs[(t + 1) * B] - offs[t * B]),), device=gpu, generator=g)
+                     for t, (E, _, _) in enumerate(specs)])
+    psw = torch.rand(idx.numel(), device=gpu, generator=g) if weighted else None
+    _say(f"[gpu] packer ty={ty} pm={pm} w={weighted}")
+    out = m(idx, off, psw).double().cpu()
+
+    def bag_sum(it, table, bo, pw, n):
+        # SUM; MEAN = weighted sum x float(1)/float(L) (P:355), not a weighted average
+        r = torch.nn.functional.embedding_bag(it, table, bo, mode="sum", per_sample_weights=pw)
+        if pm == 1:
+            L = torch.diff(torch.cat([bo, torch.tensor([n])])).clamp(min=1).double()
+            r = r / L[:, None]
+        return r
+    for t, (E, D, _) in enumerate(specs):
+        lo, hi = int(offs[t * B]), int(offs[(t + 1) * B])
+        it = idx[lo:hi].cpu()
+        bo = (offs[t * B:(t + 1) * B] - lo).cpu()
+        pw = psw[lo:hi].double().cpu() if weighted else None
+        cols = slice(int(m.D_offsets[t]), int(m.D_offsets[t + 1]))
+        got = out[:, cols]
+        # (1) the dequantised table
+        deq = torch.from_numpy(_dequantised_table(oracle, m, t))
+        n = hi - lo
+        ref = bag_sum(it, deq, bo, pw, n)
+        rowmax = deq.abs().max(1).values
+        mag = bag_sum(it, rowmax[:, None], bo, None if pw is None else pw.abs(), n)
+        assert bool(((got - ref).abs() <= 1e-5 * (mag + ref.abs()) + 1e-30).all()), f"table {t} vs dequantised"
+        # (2) the float table within the quantisation bound
+        fl = floats[t].double().cpu()
+        ref_f = bag_sum(it, fl, bo, pw, n)
+        qb = _quant_bound(m, t, floats[t].cpu())
+        bound = bag_sum(it, qb[:, None], bo, None if pw is None else pw.abs(), n)
+        err = (got - ref_f).abs()
+        assert bool((err <= bound * (1 + 1e-6) + 1e-5 * (mag + ref_f.abs())).all()), f"table {t} vs float"
+        # the quantisation is not a no-op: the bound is tight enough to matter
+        assert float(err.max()) > 0

@@ -209,3 +209,68 @@ def test_workload_specs():
     assert wl.offsets.dtype == torch.int32 and int(wl.offsets[-1]) == wl.num_indices
     wl3 = make_workload(3, device="cpu", scale_rows=0.001, batch=32)
     assert int(wl3.lengths.min()) == 0 and wl3.per_sample_weights is not None
+
+
+FP8_PARAMS = [(4, 7), (5, 15), (3, 3), (4, 8), (2, 1), (6, 31), (1, 0), (7, 60)]
+
+
+@pytest.mark.parametrize("eb,bias", FP8_PARAMS)
+def test_fp8_quantize_exact_codes_and_midpoints(pkg, oracle, eb, bias):
+    """Every code value quantises to itself (sign included); a point strictly between
+    two neighbouring codes goes to the nearer one, an exact midpoint to the even code;
+    magnitudes past the largest code saturate.  Code values come from the oracle's
+    decoder (pinned exhaustively against the closed form in test_oracle.py)."""
+    from fbgemm_ascend_amd import fp8_code_values, fp8_quantize
+    table = oracle.fp8_table(eb, bias).astype(np.float64)  # 256 codes
+    vals = fp8_code_values(eb, bias).double()
+    np.testing.assert_array_equal(vals.numpy(), table[:128])
+    codes = torch.arange(256)
+    x = torch.from_numpy(table)
+    got = fp8_quantize(x, eb, bias).to(torch.int64)
+    # +0 / -0 keep their sign bit; every other code round-trips
+    assert torch.equal(got, codes)
+    lo, hi = vals[:-1], vals[1:]
+    mid = (lo + hi) / 2
+    q = fp8_quantize(mid, eb, bias).to(torch.int64)
+    even = torch.where(torch.arange(1, 128) % 2 == 0, torch.arange(1, 128), torch.arange(0, 127))
+    assert torch.equal(q, even)
+    near_lo = lo + (hi - lo) * 0.25
+    near_hi = lo + (hi - lo) * 0.75
+    assert torch.equal(fp8_quantize(near_lo, eb, bias).to(torch.int64), torch.arange(0, 127))
+    assert torch.equal(fp8_quantize(near_hi, eb, bias).to(torch.int64), torch.arange(1, 128))
+    assert torch.equal(fp8_quantize(-near_hi, eb, bias).to(torch.int64), torch.arange(1, 128) | 0x80)
+    big = torch.tensor([float(vals[127]) * 1.5, -float(vals[127]) * 4])
+    assert fp8_quantize(big, eb, bias).tolist() == [0x7F, 0xFF]
+
+
+@pytest.mark.parametrize("eb,bias,tdt,maxfin", [(4, 7, torch.float8_e4m3fn, 448.0), (5, 15, torch.float8_e5m2, 57344.0)])
+def test_fp8_quantize_matches_torch_float8_casts(pkg, eb, bias, tdt, maxfin):
+    """Inside the finite range of torch's float8 formats (same exponent width and bias,
+    round to nearest even) the quantiser picks the same bit pattern as torch's cast."""
+    from fbgemm_ascend_amd import fp8_quantize
+    g = torch.Generator().manual_seed(eb)
+    x = (torch.rand(200000, generator=g, dtype=torch.float64) * 2 - 1) * maxfin
+    x = x * torch.exp2(-torch.randint(0, 20, x.shape, generator=g).double())
+    x = x.float()
+    want = x.to(tdt).view(torch.uint8)
+    got = fp8_quantize(x, eb, bias)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("eb,bias", FP8_PARAMS[:4])
+def test_module_fp8_quantize_roundtrip(pkg, oracle, eb, bias):
+    """load_float_weights on an FP8 table: decoded rows (oracle nobag) are within half
+    a code step of the float table."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType, fp8_code_values
+    vals = fp8_code_values(eb, bias).double()
+    w = (torch.rand(8, 64, dtype=torch.float64) * 2 - 1) * float(vals[127]) * 0.9
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(8, 64, SparseType.FP8)], device="cpu",
+                                                fp8_exponent_bits=eb, fp8_exponent_bias=bias)
+    m.load_float_weights(0, w.float())
+    out, _ = oracle.forward(m.weights_dev.numpy(), m.weights_offsets.numpy(), m.weights_tys.numpy(),
+                            m.D_offsets.numpy(), np.arange(8, dtype=np.int32), np.array([0, 8], np.int32),
+                            2, None, 0, fp8_exponent_bits=eb, fp8_exponent_bias=bias)
+    a = w.float().double().abs()
+    k = torch.searchsorted(vals, a).clamp(1, 127)
+    half_step = (vals[k] - vals[k - 1]) / 2
+    assert bool(((torch.from_numpy(out).double() - w.float().double()).abs() <= half_step).all())
