@@ -16,7 +16,9 @@ from . import HIP_LIB
 ABI_VERSION = 3
 EXPORTS = ("tbe_nbit_plan", "tbe_nbit_forward", "tbe_last_error", "tbe_nbit_abi_version",
            "tbe_permute_pooled_embs", "tbe_block_bucketize_workspace_bytes",
-           "tbe_block_bucketize_sparse_features")
+           "tbe_block_bucketize_sparse_features", "tbe_block_bucketize_sparse_features_noalloc")
+# TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES of include/tbe_sparse_ops.h
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 TBE_OK, TBE_ERR_INVALID_ARG, TBE_ERR_UNSUPPORTED, TBE_ERR_LAUNCH = 0, -1, -2, -3
 TBE_FLAG_NO_XCD_REMAP = 0x1
@@ -120,6 +122,9 @@ def lib():
         L.tbe_block_bucketize_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]
         L.tbe_block_bucketize_sparse_features.restype = ctypes.c_int
         L.tbe_block_bucketize_sparse_features.argtypes = [ctypes.POINTER(TbeBlockBucketizeArgs), ctypes.c_void_p]
+        L.tbe_block_bucketize_sparse_features_noalloc.restype = ctypes.c_int
+        L.tbe_block_bucketize_sparse_features_noalloc.argtypes = [ctypes.POINTER(TbeBlockBucketizeArgs),
+                                                                  ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -254,9 +259,10 @@ def permute_pooled_embs(pooled_embs, offset_dim_list, permute_list, inv_offset_d
 
 def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, block_sizes, my_size,
                                     weights=None, batch_size_per_feature=None, block_bucketize_pos=None,
-                                    keep_orig_idx=False, total_num_blocks=None):
+                                    keep_orig_idx=False, total_num_blocks=None, noalloc=False):
     """tbe_block_bucketize_sparse_features on torch device tensors; returns the op's
-    five outputs (None where not requested) plus new_offsets."""
+    five outputs (None where not requested) plus new_offsets.  noalloc=True calls
+    tbe_block_bucketize_sparse_features_noalloc instead (no workspace passed)."""
     import torch
 
     dev = indices.device
@@ -280,8 +286,8 @@ def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, b
         keep += ps
         pos_ptrs = torch.tensor([p.data_ptr() for p in ps], dtype=torch.int64, device=dev)
         pos_lens = torch.tensor([p.numel() for p in ps], dtype=torch.int64, device=dev)
-    wsb = lib().tbe_block_bucketize_workspace_bytes(my_size, L, lengths.element_size())
-    ws = torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
+    wsb = 0 if noalloc else lib().tbe_block_bucketize_workspace_bytes(my_size, L, lengths.element_size())
+    ws = None if noalloc else torch.empty(max(1, wsb), dtype=torch.uint8, device=dev)
     a = TbeBlockBucketizeArgs()
     ptr = lambda x: x.data_ptr() if x is not None else None  # noqa: E731
     a.indices, a.num_indices, a.offsets, a.lengths_size = ptr(indices), N, ptr(offsets), L
@@ -293,7 +299,8 @@ def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, b
     a.new_weights, a.new_pos, a.unbucketize_permute = ptr(new_w), ptr(new_pos), ptr(unb)
     a.workspace, a.workspace_bytes = ptr(ws), wsb
     stream = torch.cuda.current_stream(dev).cuda_stream if indices.is_cuda else 0
-    rc = lib().tbe_block_bucketize_sparse_features(ctypes.byref(a), ctypes.c_void_p(stream))
+    fn = lib().tbe_block_bucketize_sparse_features_noalloc if noalloc else lib().tbe_block_bucketize_sparse_features
+    rc = fn(ctypes.byref(a), ctypes.c_void_p(stream))
     if rc != TBE_OK:
         raise TbeError(rc, last_error())
     torch.cuda.synchronize(dev)  # the temporaries above must outlive the launches

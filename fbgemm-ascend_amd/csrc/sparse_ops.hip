@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "tbe_internal.h"
@@ -753,8 +754,48 @@ int64_t ws_layout(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
   return so + std::max<int64_t>(1, scan_tiles_of(my * L)) * os;
 }
 
+// Scratch of the entry point that allocates nothing
+// (tbe_block_bucketize_sparse_features_noalloc): one copy per GPU, held until the
+// process ends.  Host code never passes `scratch` itself (on the host it is only a
+// stand-in symbol); it passes the device address hipGetSymbolAddress returns.
+constexpr int64_t kNoAllocScratchBytes = TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch array (looked up once per device, with the
+// device current).  Returns nullptr and sets the error on failure.
+void* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(TBE_ERR_LAUNCH, "no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      fail(TBE_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+// Scratch bytes a call needs: the per-segment write cursors (my_size > 64 only;
+// up to 64 buckets the cursors live in registers and LDS) and the scan's tile sums.
+int64_t noalloc_need(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
+  const int64_t done_bytes = my > kWaveBB ? (my * L * 4 + 255) / 256 * 256 : 0;
+  if (sums_off) *sums_off = done_bytes;
+  return done_bytes + std::max<int64_t>(1, scan_tiles_of(my * L)) * os;
+}
+
 template <typename IT, typename OT>
-int run(const TbeBlockBucketizeArgs* a, hipStream_t s) {
+int run(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_off) {
   BBParams<IT, OT> p{};
   p.indices = static_cast<const IT*>(a->indices);
   p.offsets = static_cast<const OT*>(a->offsets);
@@ -770,10 +811,8 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s) {
   p.new_weights = a->weights ? a->new_weights : nullptr;
   p.new_pos = static_cast<IT*>(a->new_pos);
   p.unb = static_cast<IT*>(a->unbucketize_permute);
-  int64_t sums_off = 0;
-  ws_layout(a->my_size, a->lengths_size, a->offset_size, &sums_off);
-  p.done = static_cast<uint32_t*>(a->workspace);
-  OT* sums = reinterpret_cast<OT*>(static_cast<uint8_t*>(a->workspace) + sums_off);
+  p.done = static_cast<uint32_t*>(ws);
+  OT* sums = reinterpret_cast<OT*>(static_cast<uint8_t*>(ws) + sums_off);
   p.L = a->lengths_size;
   p.N = a->num_indices;
   p.my_size = a->my_size;
@@ -826,8 +865,11 @@ extern "C" int64_t tbe_block_bucketize_workspace_bytes(int64_t my_size, int64_t 
   return ws_layout(my_size, lengths_size, offset_size, nullptr);
 }
 
-extern "C" int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* a, void* hip_stream) {
-  clear_error();
+namespace tbe {
+namespace {
+
+// Argument checks shared by both entry points (BA:37-91, BA:107-128).
+int check_args(const TbeBlockBucketizeArgs* a) {
   if (!a) return fail(TBE_ERR_INVALID_ARG, "null args");
   if (a->my_size <= 0) return fail(TBE_ERR_INVALID_ARG, "my_size must be positive.");
   if ((a->index_size != 4 && a->index_size != 8) || (a->offset_size != 4 && a->offset_size != 8))
@@ -843,14 +885,51 @@ extern "C" int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* 
     return fail(TBE_ERR_UNSUPPORTED, "my_size * lengths_size must stay below 2^32");
   if (a->bucketize_pos && !a->bucketize_pos_len) return fail(TBE_ERR_INVALID_ARG, "missing bucketize_pos_len");
   if (a->weights && !a->new_weights) return fail(TBE_ERR_INVALID_ARG, "weights given without new_weights");
-  const int64_t need = ws_layout(a->my_size, a->lengths_size, a->offset_size, nullptr);
-  if (!a->workspace || a->workspace_bytes < need)
-    return fail(TBE_ERR_INVALID_ARG, "workspace of %lld bytes needed", static_cast<long long>(need));
+  return TBE_OK;
+}
+
+int check_pointers(const TbeBlockBucketizeArgs* a) {
   if (!a->new_lengths || !a->new_offsets || (a->lengths_size > 0 && (!a->offsets || !a->block_sizes)) ||
       (a->num_indices > 0 && (!a->indices || !a->new_indices)))
     return fail(TBE_ERR_INVALID_ARG, "null pointer argument");
-  hipStream_t s = static_cast<hipStream_t>(hip_stream);
+  return TBE_OK;
+}
+
+int dispatch(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_off) {
   if (a->index_size == 4)
-    return a->offset_size == 4 ? run<int32_t, int32_t>(a, s) : run<int32_t, int64_t>(a, s);
-  return a->offset_size == 4 ? run<int64_t, int32_t>(a, s) : run<int64_t, int64_t>(a, s);
+    return a->offset_size == 4 ? run<int32_t, int32_t>(a, s, ws, sums_off) : run<int32_t, int64_t>(a, s, ws, sums_off);
+  return a->offset_size == 4 ? run<int64_t, int32_t>(a, s, ws, sums_off) : run<int64_t, int64_t>(a, s, ws, sums_off);
+}
+
+}  // namespace
+}  // namespace tbe
+
+extern "C" int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* a, void* hip_stream) {
+  clear_error();
+  const int rc = check_args(a);
+  if (rc != TBE_OK) return rc;
+  int64_t sums_off = 0;
+  const int64_t need = ws_layout(a->my_size, a->lengths_size, a->offset_size, &sums_off);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(TBE_ERR_INVALID_ARG, "workspace of %lld bytes needed", static_cast<long long>(need));
+  if (check_pointers(a) != TBE_OK) return TBE_ERR_INVALID_ARG;
+  return dispatch(a, static_cast<hipStream_t>(hip_stream), a->workspace, sums_off);
+}
+
+extern "C" int tbe_block_bucketize_sparse_features_noalloc(const TbeBlockBucketizeArgs* a, void* hip_stream) {
+  clear_error();
+  const int rc = check_args(a);
+  if (rc != TBE_OK) return rc;
+  int64_t sums_off = 0;
+  const int64_t need = noalloc_need(a->my_size, a->lengths_size, a->offset_size, &sums_off);
+  if (need > kNoAllocScratchBytes)
+    return fail(TBE_ERR_UNSUPPORTED,
+                "block_bucketize_sparse_features_noalloc: this call needs %lld bytes of scratch, more than the "
+                "%lld the library holds per GPU (my_size * lengths_size too large); use "
+                "tbe_block_bucketize_sparse_features with a workspace",
+                static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+  if (check_pointers(a) != TBE_OK) return TBE_ERR_INVALID_ARG;
+  void* ws = scratch_for_current_device();
+  if (!ws) return TBE_ERR_LAUNCH;
+  return dispatch(a, static_cast<hipStream_t>(hip_stream), ws, sums_off);
 }

@@ -80,6 +80,28 @@ int64_t tbe_block_bucketize_workspace_bytes(int64_t my_size, int64_t lengths_siz
 
 int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* args, void* hip_stream);
 
+/*
+ * Same operation and results as tbe_block_bucketize_sparse_features, without any
+ * allocation: no hipMalloc / hipFree / allocating library call, and no workspace
+ * argument (args->workspace and args->workspace_bytes are ignored).  It has no
+ * counterpart in the reference; it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it).  The
+ * caller still passes every input and output.
+ *
+ * Scratch (the per-segment write cursors when my_size > 64, and the scan's tile
+ * sums) lives in a static device array of TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES
+ * bytes that each GPU the library runs on holds until the process ends; it is
+ * cleared by the call's own kernels where it must start at zero.  A call needs
+ *   (my_size > 64 ? roundup(4 * my_size * lengths_size, 256) : 0)
+ *   + offset_size * max(1, ceil(my_size * lengths_size / 1024))
+ * bytes of it; larger calls are rejected with TBE_ERR_UNSUPPORTED and a message.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on
+ * one GPU (on different streams, or from several threads without ordering) race
+ * on it and give wrong results.  Calls queued on one stream are ordered and safe.
+ */
+#define TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES (32LL << 20)
+int tbe_block_bucketize_sparse_features_noalloc(const TbeBlockBucketizeArgs* args, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

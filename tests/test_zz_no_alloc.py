@@ -1,0 +1,64 @@
+"""GPU: tbe_block_bucketize_sparse_features_noalloc (no allocation, static scratch)
+gives exactly the outputs of tbe_block_bucketize_sparse_features (workspace
+argument), through the C ABI, on two calls in a row, the second with a smaller
+input, for register-cursor (my_size <= 64) and memory-cursor (my_size > 64)
+bucket counts; a call that needs more scratch than the library holds is rejected."""
+import numpy as np
+import pytest
+import torch
+
+from _bucketize_cases import CASES, Case, gen_bucketize_pos, gen_case
+
+pytestmark = pytest.mark.gpu
+
+BY_NAME = {c.name: c for c in CASES}
+WIDE = Case("i64_rank100", 6, 512, 0, 96, 4, 8, 100, np.int64)
+WIDE_SMALL = Case("i32_rank70", 3, 64, 0, 40, 2, 6, 70, np.int32)
+
+
+def _run(gpu, case, seed, noalloc, weights, bucketize_pos, sequence, pos):
+    from fbgemm_ascend_amd import capi
+    lengths, indices, block_sizes, w = gen_case(case, seed, weights)
+    d = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    plist = [d(p) for p in gen_bucketize_pos(block_sizes, case.my_size, seed)] if pos else None
+    outs, new_off = capi.block_bucketize_sparse_features(
+        d(lengths), d(indices), bucketize_pos, sequence, d(block_sizes), case.my_size, weights=d(w),
+        block_bucketize_pos=plist, noalloc=noalloc)
+    torch.cuda.synchronize()
+    return [None if o is None else o.cpu() for o in outs] + [new_off.cpu()]
+
+
+PAIRS = [("i64_stress", "i32_pow2_basic"), ("i64_rank64", "i64_nonpow2_rank5"), ("WIDE", "WIDE_SMALL"),
+         ("i32_many_features", "i32_mysize1")]
+
+
+@pytest.mark.parametrize("big,small", PAIRS)
+@pytest.mark.parametrize("weights,bucketize_pos,sequence,pos", [(False, False, False, False),
+                                                                (True, True, True, False),
+                                                                (True, False, True, True)])
+def test_noalloc_matches_workspace_entry(pkg, gpu, big, small, weights, bucketize_pos, sequence, pos):
+    names = ["new_lengths", "new_indices", "new_weights", "new_pos", "unbucketize_permute", "new_offsets"]
+    cases = {"WIDE": WIDE, "WIDE_SMALL": WIDE_SMALL, **BY_NAME}
+    for step, name in enumerate((big, small)):
+        case = cases[name]
+        seed = 100 + step
+        print(f"[gpu] noalloc call {step + 1}: {name} my_size={case.my_size} w={weights} pos={bucketize_pos} "
+              f"seq={sequence} poslist={pos}", flush=True)
+        got = _run(gpu, case, seed, True, weights, bucketize_pos, sequence, pos)
+        want = _run(gpu, case, seed, False, weights, bucketize_pos, sequence, pos)
+        for n, g, e in zip(names, got, want):
+            assert (g is None) == (e is None), n
+            if e is not None:
+                assert torch.equal(g, e), f"{name}: {n} differs"
+
+
+def test_noalloc_rejects_oversized_calls(pkg, gpu):
+    from fbgemm_ascend_amd import capi
+    my, L = 2000, 5000  # 40 MB of write cursors > the 32 MiB scratch
+    lengths = torch.ones(L, dtype=torch.int32, device=gpu)
+    indices = torch.arange(L, dtype=torch.int32, device=gpu)
+    bs = torch.full((1,), 4, dtype=torch.int32, device=gpu)
+    with pytest.raises(capi.TbeError, match="scratch"):
+        capi.block_bucketize_sparse_features(lengths, indices, False, False, bs, my, noalloc=True)
+    # the same call fits the workspace entry point
+    capi.block_bucketize_sparse_features(lengths, indices, False, False, bs, my)
