@@ -8,10 +8,18 @@ random permutation per table), int32 indices/offsets, SUM pooling, fp16 output
 torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function over that batch,
 with every input resident in HBM before the timed region starts.
 
+The timed loop rotates over --batches (default 4) distinct batches drawn from the
+same distributions (every table keeps its Zipf rank -> row map), all resident in
+HBM before timing, so each call meets the cache state a stream of fresh requests
+leaves; the same batch replayed back to back and a cache-scrubbed call are reported
+beside it (`replay_same_batch`, `cold_cache`).
+
 Prints ONE JSON line.  `value` = pooled lookups per second; `roofline` prices the
 kernel's algorithmic bytes (unpadded rows of every lookup + indices + offsets +
 output) per launch against the 8 TB/s HBM peak; `cpu_baseline` times the C oracle
-(OpenMP) on a bounded sample of the same workload on this host's cores.
+(OpenMP) on a bounded sample of the same workload on this host's cores, reading the
+whole tables from host memory; `cpu_baseline_library` times torch's FBGEMM CPU
+kernels (torch.ops.quantized.embedding_bag_*_rowwise_offsets) on the same sample.
 """
 from __future__ import annotations
 
@@ -36,6 +44,9 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target wall time of the CPU leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache measurement")
+    ap.add_argument("--no-replay", action="store_true", help="skip the same-batch replay measurement")
+    ap.add_argument("--batches", type=int, default=4,
+                    help="distinct batches generated before timing and rotated in the timed loop")
     ap.add_argument("--flags", type=int, default=0, help="TBE_FLAG_* tuning switches (C-ABI path)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB device copy instead (calibrates rocprof FETCH/WRITE_SIZE)")
@@ -160,47 +171,168 @@ def bench_nobag(args, pkg, dev):
     print(json.dumps(out), flush=True)
 
 
-def _cpu_cores():
+def _cpu_threads():
+    """Host threads of the CPU legs: the process's CPU affinity, capped by OMP_NUM_THREADS
+    when it is set (the GPU boxes set it to their per-GPU CPU share)."""
     try:
-        return len(os.sched_getaffinity(0))
+        n = len(os.sched_getaffinity(0))
     except AttributeError:
-        return os.cpu_count() or 1
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return n
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# host copies of the tables above this size are not made; the CPU legs then run on
+# the referenced rows only (and say so)
+_HOST_TABLE_LIMIT = 32 << 30
+
+
+def _sample_bags(wl, nsamp):
+    """Indices/offsets/weights of the first `nsamp` samples of every table (host arrays,
+    original row ids), in the op's table-major bag order."""
+    import numpy as np
+    T = len(wl.module.specs)
+    B = wl.spec.B
+    off = wl.offsets.cpu().numpy().astype(np.int64)
+    idx = wl.indices.cpu().numpy()
+    psw = wl.per_sample_weights.cpu().numpy() if wl.per_sample_weights is not None else None
+    parts, wparts, new_off = [], [], [0]
+    for t in range(T):
+        lo, hi = off[t * B], off[t * B + nsamp]
+        parts.append(idx[lo:hi])
+        if psw is not None:
+            wparts.append(psw[lo:hi])
+        new_off.extend((off[t * B + 1:t * B + nsamp + 1] - lo + new_off[-1]).tolist())
+    s_idx = np.concatenate(parts)
+    s_off = np.asarray(new_off, dtype=idx.dtype)
+    s_psw = np.concatenate(wparts) if psw is not None else None
+    return s_idx, s_off, s_psw
 
 
 def cpu_baseline(wl, target_s: float):
-    """Time the C oracle on a bounded sample of the workload (whole bags, all tables)."""
+    """Time the C oracle (OpenMP) on a bounded sample of the workload: the first B/8 samples
+    of every table, reading rows from a host copy of the whole dev_weights buffer."""
     import numpy as np
     import torch
     import __graft_entry__ as graft
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from _parity import compact_problem, run_oracle
 
     oracle = graft.load_oracle()
-    cores = min(_cpu_cores(), 16)
+    cores = _cpu_threads()
+    m = wl.module
     B = wl.spec.B
     nsamp = max(1, B // 8)
-    g = torch.Generator(device=wl.indices.device)
-    g.manual_seed(17)
-    b_sel = torch.randperm(B, device=wl.indices.device, generator=g)[:nsamp].sort().values
-    prob = compact_problem(wl.module, wl.indices, wl.offsets, wl.per_sample_weights, b_sel)
+    pm = int(m.pooling_mode)
+    bits, bias = m.fp8_exponent_bits, m.fp8_exponent_bias
+    if m.weights_dev.numel() <= _HOST_TABLE_LIMIT:
+        weights = m.weights_dev.cpu().numpy()
+        s_idx, s_off, s_psw = _sample_bags(wl, nsamp)
+        prob = dict(weights=weights, weights_offsets=m.weights_offsets.cpu().numpy(),
+                    weights_tys=m.weights_tys.cpu().numpy(), D_offsets=m.D_offsets.cpu().numpy(),
+                    indices=s_idx, offsets=s_off, psw=s_psw)
+        layout = "whole tables in host memory"
+    else:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        from _parity import compact_problem
+        g = torch.Generator(device=wl.indices.device)
+        g.manual_seed(17)
+        b_sel = torch.arange(nsamp, device=wl.indices.device)
+        prob = compact_problem(m, wl.indices, wl.offsets, wl.per_sample_weights, b_sel)
+        layout = "compacted: only the sample's referenced rows copied to host (tables exceed host copy limit)"
     n_lookups = int(prob["offsets"][-1])
-    pm = int(wl.module.pooling_mode)
-    run_oracle(oracle, prob, pm, wl.module.output_dtype)  # warm the host caches / page in
+
+    def run():
+        oracle.forward(prob["weights"], prob["weights_offsets"], prob["weights_tys"], prob["D_offsets"],
+                       prob["indices"], prob["offsets"], pm, prob["psw"], m.output_dtype,
+                       fp8_exponent_bits=bits, fp8_exponent_bias=bias, num_threads=cores)
+
+    run()  # page in
     reps, t0 = 0, time.perf_counter()
     while True:
-        bits, bias = prob["fp8"]
-        oracle.forward(prob["weights"], prob["weights_offsets"], prob["weights_tys"], prob["D_offsets"],
-                       prob["indices"], prob["offsets"], pm, prob["psw"], wl.module.output_dtype,
-                       fp8_exponent_bits=bits, fp8_exponent_bias=bias, num_threads=cores)
+        run()
         reps += 1
         el = time.perf_counter() - t0
-        if el >= target_s or reps >= 1000:
+        if el >= target_s or reps >= 100000:
             break
-    rate = n_lookups * reps / el
-    return {"value": rate, "unit": "pooled lookups/s", "cores": cores, "kind": "port",
-            "sample": f"{nsamp} of {B} samples x {len(wl.module.specs)} tables "
-                      f"({n_lookups} lookups, rows gathered to host), {reps} reps in {el:.1f}s, "
-                      f"oracle/tbe_oracle.c OpenMP fp32"}
+    res = {"value": n_lookups * reps / el, "unit": "pooled lookups/s", "cores": cores, "kind": "port",
+           "sample": f"first {nsamp} of {B} samples x {len(m.specs)} tables ({n_lookups} lookups), {layout}, "
+                     f"{reps} reps in {el:.1f}s, oracle/tbe_oracle.c OpenMP fp32 on {cores} threads "
+                     f"(process affinity capped by OMP_NUM_THREADS, the box's per-GPU CPU share)",
+           "cpu_model": _cpu_model()}
+    lib = library_baseline(wl, prob, cores, target_s) if layout.startswith("whole") else None
+    return res, lib
+
+
+def library_baseline(wl, prob, cores: int, target_s: float):
+    """torch.ops.quantized.embedding_bag_{byte,4bit}_rowwise_offsets (FBGEMM's CPU kernels
+    shipped with torch), one call per table, on the same sample and whole tables repacked to
+    the scale/bias-last row layout those kernels read.  Unweighted SUM over uniform INT8/INT4
+    tables only; returns None otherwise.  Its output is fp32 (no fp16 cast)."""
+    import numpy as np
+    import torch
+
+    m = wl.module
+    tys = {int(ty) for (_, _, ty) in m.specs}
+    if len(tys) != 1 or tys.pop() not in (2, 3) or wl.per_sample_weights is not None or int(m.pooling_mode) != 0:
+        return None
+    ty = int(m.specs[0][2])
+    fn = (torch.ops.quantized.embedding_bag_byte_rowwise_offsets if ty == 2
+          else torch.ops.quantized.embedding_bag_4bit_rowwise_offsets)
+    w = prob["weights"]
+    wo = prob["weights_offsets"]
+    T = len(m.specs)
+    Bs = (len(prob["offsets"]) - 1) // T
+    off = prob["offsets"].astype(np.int64)
+    idx = prob["indices"].astype(np.int64)
+    tables, calls = [], []
+    for t, (E, D, _) in enumerate(m.specs):
+        payload = D if ty == 2 else D // 2
+        stride = int(m.row_strides[t])
+        rows = w[wo[t]:wo[t] + E * stride].reshape(E, stride)
+        if ty == 2:  # fp32 scale and bias after the codes
+            sb = np.empty((E, 2), dtype=np.float32)
+            sb[:, 0] = rows[:, 0:2].copy().view(np.float16)[:, 0]
+            sb[:, 1] = rows[:, 2:4].copy().view(np.float16)[:, 0]
+            lib = np.concatenate([rows[:, 4:4 + payload], sb.view(np.uint8).reshape(E, 8)], 1)
+        else:        # fp16 scale and bias after the codes
+            lib = np.concatenate([rows[:, 4:4 + payload], rows[:, 0:4]], 1)
+        tables.append(torch.from_numpy(np.ascontiguousarray(lib)))
+        lo, hi = off[t * Bs], off[(t + 1) * Bs]
+        calls.append((torch.from_numpy(idx[lo:hi]), torch.from_numpy(off[t * Bs:(t + 1) * Bs + 1] - lo)))
+    n_lookups = int(off[-1] - off[0])
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        def run():
+            for tab, (i, o) in zip(tables, calls):
+                fn(tab, i, o, False, 0, False, None, None, True)
+        run()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            run()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= target_s or reps >= 100000:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": n_lookups * reps / el, "unit": "pooled lookups/s", "cores": cores, "kind": "library",
+            "sample": f"same sample as cpu_baseline ({n_lookups} lookups), whole tables repacked, "
+                      f"torch.ops.quantized.embedding_bag_{'byte' if ty == 2 else '4bit'}_rowwise_offsets "
+                      f"per table, fp32 out, {reps} reps in {el:.1f}s, torch.set_num_threads({cores})",
+            "cpu_model": _cpu_model()}
 
 
 def bench_bucketize(args, pkg, dev):
@@ -296,36 +428,52 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(),
                           "calls": args.warmup + args.steps}), flush=True)
         return
-    wl = make_workload(args.config, device=dev)
+    wl = make_workload(args.config, device=dev, num_batches=max(1, args.batches))
     m = wl.module
+    K = len(wl.batches)
     torch.cuda.synchronize()
 
     if args.flags:
         # C-ABI path with tuning switches: plan, upload and output allocation happen once here
-        step = pkg.capi.prepare_forward(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets,
-                                        wl.indices, wl.offsets, int(m.pooling_mode), wl.per_sample_weights,
-                                        m.output_dtype, flags=args.flags)
+        calls = [pkg.capi.prepare_forward(m.weights_dev, m.weights_offsets, m.weights_tys, m.D_offsets,
+                                          bt.indices, bt.offsets, int(m.pooling_mode), bt.per_sample_weights,
+                                          m.output_dtype, flags=args.flags) for bt in wl.batches]
     else:
-        step = wl.run
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
+        calls = [(lambda i=i: wl.run(i)) for i in range(K)]
+    lookups = [wl.num_indices_of(i) for i in range(K)]
+    alg = [wl.algorithmic_bytes(i) for i in range(K)]
     stream = torch.cuda.current_stream(dev)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
+
+    def timed(order):
+        """HIP events around every call on the launch stream; returns (per-call ms, wall s)."""
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for (a, b), i in zip(evs, order):
+            a.record(stream)
+            calls[i]()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) for a, b in evs], time.perf_counter() - t0
+
+    for s in range(args.warmup):
+        calls[s % K]()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for a, b in evs:
-        a.record(stream)
-        step()
-        b.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_call_ms = sorted(a.elapsed_time(b) for a, b in evs)
+
+    # headline: a stream of distinct batches from the same distributions (batch s % K)
+    order = [s % K for s in range(args.steps)]
+    per_call_ms, wall = timed(order)
     kernel_ms = sum(per_call_ms) / len(per_call_ms)
     ms_per_step = wall * 1e3 / args.steps
+    total_lookups = sum(lookups[i] for i in order)
+    total_alg = sum(alg[i] for i in order)
+    achieved = total_alg / (sum(per_call_ms) * 1e-3) / 1e9
+
+    # the same batch replayed back to back (L2 and MALL hold the previous call's rows)
+    replay_kernel_ms = None
+    if not args.no_replay:
+        replay_ms, _ = timed([0] * args.steps)
+        replay_kernel_ms = sum(replay_ms) / len(replay_ms)
 
     cold_ms = None
     if not args.no_cold:
@@ -335,28 +483,28 @@ def main():
             scrub.fill_(i & 0xFF)  # evict L2 and MALL between calls
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            step()
+            calls[i % K]()
             b.record(stream)
             torch.cuda.synchronize()
-            cold.append(a.elapsed_time(b))
-        cold_ms = sorted(cold)[len(cold) // 2]
+            cold.append((a.elapsed_time(b), i % K))
+        cold_ms = sum(c for c, _ in cold) / len(cold)
+        cold_alg = sum(alg[i] for _, i in cold) / len(cold)
         del scrub
 
-    N = wl.num_indices
-    bags = wl.num_bags
-    alg_bytes = wl.algorithmic_bytes()
-    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     traffic = None
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"tbe_cfg{args.config}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             t = json.load(f)
-        if t.get("config") == args.config:
+        if t.get("config") == args.config and t.get("batches") == K:
             traffic = t.get("hbm_bytes_per_launch")
+
+    def frac(ms, nbytes):
+        return nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS
 
     res = {
         "metric": "pooled lookups/sec + achieved HBM GB/s (% roofline), INT4/INT8 TBE fwd, 1 GPU",
-        "value": N / (ms_per_step * 1e-3),
+        "value": total_lookups / wall,
         "unit": "pooled lookups/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -366,26 +514,28 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {2: "int8", 3: "int4"}.get(int(m.specs[0][2]), "mixed") if args.config != 3 else "mixed",
-        "data": "synthetic (seeded, generated on device)",
+        "data": f"synthetic (seeded, generated on device); {K} distinct batches from the same "
+                "distributions, rotated (step s uses batch s % K)",
         "config": {"workload": f"config{args.config}: {wl.spec.description}",
                    "tables": len(m.specs), "rows_per_table": m.specs[0][0] if args.config != 3 else "mixed",
                    "D": m.specs[0][1] if args.config != 3 else "mixed", "batch": wl.spec.B,
                    "bag_len": wl.spec.bag_len, "zipf_alpha": wl.spec.zipf_alpha,
                    "index_dtype": str(wl.indices.dtype).replace("torch.", ""),
                    "pooling": wl.spec.pooling.name, "output": {0: "fp32", 1: "fp16", 5: "bf16"}[m.output_dtype],
-                   "lookups_per_step": N, "bags_per_step": bags},
+                   "batches": K, "lookups_per_step": total_lookups / args.steps, "bags_per_step": wl.num_bags},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
         "kernel_ms": kernel_ms,
-        "kernel_ms_median": per_call_ms[len(per_call_ms) // 2],
-        "cold_cache_kernel_ms": cold_ms,
-        "algorithmic_bytes_per_step": alg_bytes,
-        "bags_per_s": bags / (ms_per_step * 1e-3),
+        "kernel_ms_median": sorted(per_call_ms)[len(per_call_ms) // 2],
+        "algorithmic_bytes_per_step": total_alg / args.steps,
+        "bags_per_s": wl.num_bags * args.steps / wall,
+        "replay_same_batch": ({"kernel_ms": replay_kernel_ms, "frac": frac(replay_kernel_ms, alg[0])}
+                              if replay_kernel_ms is not None else None),
+        "cold_cache": ({"kernel_ms": cold_ms, "frac": frac(cold_ms, cold_alg)} if cold_ms is not None else None),
     }
+    res["cpu_baseline"], res["cpu_baseline_library"] = (None, None)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
-    else:
-        res["cpu_baseline"] = None
+        res["cpu_baseline"], res["cpu_baseline_library"] = cpu_baseline(wl, args.cpu_seconds)
     print(json.dumps(res), flush=True)
 
 

@@ -46,19 +46,46 @@ HIP_SOURCES = ["tbe_nbit.hip", "tbe_kern_int4.hip", "tbe_kern_int8.hip", "tbe_ke
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 
 
-def build_hip_lib():
-    """Compile every HIP source to an object (in parallel), then link one .so."""
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer: every flag goes to the host
+# compilation only (device code is built exactly as in the product library).
+SANITIZE_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-g"]
+ASAN_DIR = os.path.join(PKG_DIR, "_asan")
+ASAN_LIB = os.path.join(ASAN_DIR, "libtbe_hip.so")
+
+
+def asan_runtime() -> str:
+    """clang's shared ASan runtime (holds the UBSan handlers too); preload it into the
+    process that loads ASAN_LIB."""
+    import glob
+    hits = sorted(glob.glob(os.path.join(ROCM, "llvm", "lib", "clang", "*", "lib", "linux",
+                                         "libclang_rt.asan-x86_64.so")))
+    if not hits:
+        raise FileNotFoundError("clang ASan runtime not found under " + ROCM)
+    return hits[-1]
+
+
+def build_hip_lib(sanitize: bool = False):
+    """Compile every HIP source to an object (in parallel), then link one .so
+    (sanitize: the host-sanitizer variant, into _asan/)."""
     from concurrent.futures import ThreadPoolExecutor
 
-    os.makedirs(OBJ_DIR, exist_ok=True)
+    obj_dir = OBJ_DIR + ("_asan" if sanitize else "")
+    out = ASAN_LIB if sanitize else HIP_LIB
+    extra = SANITIZE_FLAGS if sanitize else []
+    os.makedirs(obj_dir, exist_ok=True)
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
-    cmds = [[hipcc, *HIP_FLAGS, "-c", f"-I{INCLUDE}", f"-I{CSRC}", os.path.join(CSRC, s), "-o", o]
+    objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in HIP_SOURCES]
+    cmds = [[hipcc, *HIP_FLAGS, *extra, "-c", f"-I{INCLUDE}", f"-I{CSRC}", os.path.join(CSRC, s), "-o", o]
             for s, o in zip(HIP_SOURCES, objs)]
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         for f in [ex.submit(_run, c) for c in cmds]:
             f.result()
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", *objs, "-o", HIP_LIB])
+    link = [hipcc, f"--offload-arch={ARCH}", "-shared", *objs, "-o", out]
+    if sanitize:
+        link[2:2] = ["-fsanitize=address,undefined", "-shared-libsan"]
+    _run(link)
 
 
 def build_torch_binding():
@@ -83,6 +110,15 @@ def build():
     build_torch_binding()
 
 
+def build_sanitized():
+    """The host-sanitizer library (_asan/libtbe_hip.so) and oracle (oracle/_build_asan/)."""
+    build_hip_lib(sanitize=True)
+    _run(["make", "-s", "-C", os.path.join(REPO, "oracle"), "asan"])
+
+
 if __name__ == "__main__":
-    build()
+    if "--sanitize" in sys.argv[1:]:
+        build_sanitized()
+    else:
+        build()
     sys.exit(0)

@@ -100,13 +100,20 @@ class TbeBlockBucketizeArgs(ctypes.Structure):
 _lib = None
 
 
+def lib_path() -> str:
+    """The libtbe_hip.so this binding loads: the package's own, or the build named by
+    TBE_HIP_LIB (e.g. the host-sanitizer build of build.py --sanitize)."""
+    return os.environ.get("TBE_HIP_LIB") or HIP_LIB
+
+
 def lib():
     """Load libtbe_hip.so (loading needs no GPU; launching does)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(HIP_LIB):
-            raise FileNotFoundError(f"{HIP_LIB} is not built")
-        L = ctypes.CDLL(HIP_LIB)
+        path = lib_path()
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built")
+        L = ctypes.CDLL(path)
         L.tbe_nbit_plan.restype = ctypes.c_int
         L.tbe_nbit_plan.argtypes = [ctypes.POINTER(TbePlanInput), ctypes.POINTER(TbeTableDesc),
                                     ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(TbePlanSummary)]

@@ -191,8 +191,13 @@ Tensor int_nbit_split_embedding_codegen_lookup_function_hip(
   TORCH_CHECK(pooling_mode >= TBE_POOL_SUM && pooling_mode <= TBE_POOL_NONE, "Invalid pooling mode ",
               pooling_mode, ": supported modes are SUM(0), MEAN(1), NONE(2)");
   const at::ScalarType out_type = sparse_type_to_scalar_type(output_dtype);
-  TORCH_CHECK(output_dtype != TBE_TY_INT8,
-              "INT8 output_dtype is not supported (the reference kernel asserts on it as well)");
+  if (output_dtype == TBE_TY_INT8) {
+    // A:125-129 first (same message), then the kernels' own rejection (P:336-338, N:295-296);
+    // this path only ever raises, so its host copy costs nothing in steady state
+    const bool all_int8 = weights_tys.to(at::kCPU).eq(static_cast<uint8_t>(TBE_TY_INT8)).all().item<bool>();
+    TORCH_CHECK(all_int8, "int8 output_dtype requires all tables to use int8 weights.");
+    TORCH_CHECK(false, "INT8 output_dtype is not supported (the reference kernel asserts on it as well)");
+  }
 
   const PlanKey key{weights_offsets.data_ptr(), static_cast<int64_t>(weights_offsets._version()),
                     weights_tys.data_ptr(),     static_cast<int64_t>(weights_tys._version()),

@@ -107,18 +107,26 @@ def _zipf_cdf(n: int, alpha: float, device) -> torch.Tensor:
     return c
 
 
+def _table_perm(n_rows: int, perm_seed: int, device) -> torch.Tensor:
+    """Rank -> row map of one table: fixed by the table's seed, so every batch drawn
+    from the table sees the same hot rows."""
+    g = torch.Generator(device=device)
+    g.manual_seed(perm_seed)
+    return torch.randperm(n_rows, device=device, generator=g)
+
+
 def sample_rows(n_rows: int, count: int, alpha: Optional[float], tail: float,
-                g: torch.Generator, device) -> torch.Tensor:
-    """`count` row ids of one table: Zipf(alpha) ranks scattered by a random permutation
-    (with a `tail` fraction drawn uniformly), or uniform when alpha is None."""
+                g: torch.Generator, device, perm_seed: int = 0) -> torch.Tensor:
+    """`count` row ids of one table: Zipf(alpha) ranks scattered by the table's fixed
+    permutation (seeded by `perm_seed`, with a `tail` fraction drawn uniformly), or
+    uniform when alpha is None."""
     if count == 0:
         return torch.empty(0, dtype=torch.int64, device=device)
     if alpha is None:
         return torch.randint(0, n_rows, (count,), dtype=torch.int64, device=device, generator=g)
     u = torch.rand(count, dtype=torch.float64, device=device, generator=g)
     ranks = torch.searchsorted(_zipf_cdf(n_rows, alpha, device), u).clamp_(max=n_rows - 1)
-    perm = torch.randperm(n_rows, device=device, generator=g)
-    rows = perm[ranks]
+    rows = _table_perm(n_rows, perm_seed, device)[ranks]
     if tail > 0:
         pick = torch.rand(count, device=device, generator=g) < tail
         uni = torch.randint(0, n_rows, (count,), dtype=torch.int64, device=device, generator=g)
@@ -127,43 +135,92 @@ def sample_rows(n_rows: int, count: int, alpha: Optional[float], tail: float,
 
 
 @dataclasses.dataclass
-class Workload:
-    spec: ConfigSpec
-    module: IntNBitTableBatchedEmbeddingBagsCodegen
+class Batch:
+    """One batch of the op's sparse inputs."""
     indices: torch.Tensor
     offsets: torch.Tensor
     per_sample_weights: Optional[torch.Tensor]
     lengths: torch.Tensor          # int64 [T*B]
 
+
+@dataclasses.dataclass
+class Workload:
+    spec: ConfigSpec
+    module: IntNBitTableBatchedEmbeddingBagsCodegen
+    batches: List[Batch]           # batch 0 first; all drawn from the same distributions
+
+    @property
+    def indices(self) -> torch.Tensor:
+        return self.batches[0].indices
+
+    @property
+    def offsets(self) -> torch.Tensor:
+        return self.batches[0].offsets
+
+    @property
+    def per_sample_weights(self) -> Optional[torch.Tensor]:
+        return self.batches[0].per_sample_weights
+
+    @property
+    def lengths(self) -> torch.Tensor:
+        return self.batches[0].lengths
+
+    def num_indices_of(self, i: int = 0) -> int:
+        return int(self.batches[i].indices.numel())
+
     @property
     def num_indices(self) -> int:
-        return int(self.indices.numel())
+        return self.num_indices_of(0)
 
     @property
     def num_bags(self) -> int:
         return int(self.offsets.numel() - 1)
 
-    def algorithmic_bytes(self) -> int:
-        """Bytes one call must move at minimum: every lookup's unpadded row, the indices,
-        offsets, per-sample weights and the output."""
+    def algorithmic_bytes(self, i: int = 0) -> int:
+        """Bytes one call on batch i must move at minimum: every lookup's unpadded row,
+        the indices, offsets, per-sample weights and the output."""
+        bt = self.batches[i]
         T = len(self.module.specs)
-        per_table = self.lengths.view(T, -1).sum(dim=1).cpu().tolist()
+        per_table = bt.lengths.view(T, -1).sum(dim=1).cpu().tolist()
         rows = sum(int(c) * unpadded_row_bytes(ty, D)
                    for c, (_, D, ty) in zip(per_table, self.module.specs))
-        isz = self.indices.element_size()
+        isz = bt.indices.element_size()
         out_sz = {0: 4, 1: 2, 5: 2}[self.module.output_dtype]
-        b = rows + self.num_indices * isz + self.offsets.numel() * isz
-        if self.per_sample_weights is not None:
-            b += 4 * self.num_indices
+        b = rows + bt.indices.numel() * isz + bt.offsets.numel() * isz
+        if bt.per_sample_weights is not None:
+            b += 4 * bt.indices.numel()
         b += self.spec.B * self.module.total_D * out_sz
         return b
 
-    def run(self) -> torch.Tensor:
-        return self.module(self.indices, self.offsets, self.per_sample_weights)
+    def run(self, i: int = 0) -> torch.Tensor:
+        bt = self.batches[i]
+        return self.module(bt.indices, bt.offsets, bt.per_sample_weights)
+
+
+def make_batch(spec: ConfigSpec, seed: int, device) -> Batch:
+    """Bag lengths, indices (and weights) of one batch; table t's Zipf permutation is
+    seeded by (config, t) alone, so batches of one config share their hot rows."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    T = len(spec.tables)
+    lengths = _bag_lengths(spec, T, g, device)
+    per_table = lengths.view(T, spec.B).sum(dim=1).cpu().tolist()
+    parts = [sample_rows(E, int(c), spec.zipf_alpha, spec.uniform_tail, g, device,
+                         perm_seed=(0x7BE0 + spec.cid) * 1000 + t)
+             for t, ((E, _, _), c) in enumerate(zip(spec.tables, per_table))]
+    indices = torch.cat(parts).to(spec.index_dtype)
+    offsets = torch.zeros(T * spec.B + 1, dtype=torch.int64, device=device)
+    torch.cumsum(lengths, 0, out=offsets[1:])
+    offsets = offsets.to(spec.index_dtype)
+    psw = (torch.rand(indices.numel(), device=device, generator=g) if spec.weighted else None)
+    return Batch(indices, offsets, psw, lengths)
 
 
 def make_workload(cid: int, device="cuda", seed: Optional[int] = None, scale_rows: float = 1.0,
-                  batch: Optional[int] = None, table_limit: Optional[int] = None) -> Workload:
+                  batch: Optional[int] = None, table_limit: Optional[int] = None,
+                  num_batches: int = 1) -> Workload:
+    """Tables of configuration `cid` (random weights) and `num_batches` batches of
+    indices drawn from the configuration's distributions (distinct seeds)."""
     spec = config_spec(cid, scale_rows)
     if batch is not None:
         spec = dataclasses.replace(spec, B=batch)
@@ -174,16 +231,5 @@ def make_workload(cid: int, device="cuda", seed: Optional[int] = None, scale_row
     mod = IntNBitTableBatchedEmbeddingBagsCodegen(spec.tables, device=device, pooling_mode=spec.pooling,
                                                   output_dtype=spec.out_ty, indices_dtype=spec.index_dtype)
     mod.fill_random_weights(seed)
-    g = torch.Generator(device=device)
-    g.manual_seed(seed + 1)
-    T = len(spec.tables)
-    lengths = _bag_lengths(spec, T, g, device)
-    per_table = lengths.view(T, spec.B).sum(dim=1).cpu().tolist()
-    parts = [sample_rows(E, int(c), spec.zipf_alpha, spec.uniform_tail, g, device)
-             for (E, _, _), c in zip(spec.tables, per_table)]
-    indices = torch.cat(parts).to(spec.index_dtype)
-    offsets = torch.zeros(T * spec.B + 1, dtype=torch.int64, device=device)
-    torch.cumsum(lengths, 0, out=offsets[1:])
-    offsets = offsets.to(spec.index_dtype)
-    psw = (torch.rand(indices.numel(), device=device, generator=g) if spec.weighted else None)
-    return Workload(spec, mod, indices, offsets, psw, lengths)
+    batches = [make_batch(spec, seed + 1 + 7919 * i, device) for i in range(num_batches)]
+    return Workload(spec, mod, batches)

@@ -31,9 +31,12 @@ def build() -> str:
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB_PATH):
-            build()
-        L = ctypes.CDLL(_LIB_PATH)
+        path = os.environ.get("TBE_ORACLE_LIB")  # e.g. the sanitizer build (make asan)
+        if not path:
+            path = _LIB_PATH
+            if not os.path.exists(path):
+                build()
+        L = ctypes.CDLL(path)
         P, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
         L.oracle_tbe_forward.restype = ctypes.c_int
         L.oracle_tbe_forward.argtypes = [P, ctypes.c_int, P, P, P, P, P, P, ctypes.c_int, i64, i64,

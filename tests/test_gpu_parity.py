@@ -366,8 +366,18 @@ def test_validation_errors(pkg, gpu):
         call(offsets=off[:4])
     with pytest.raises(RuntimeError, match="Unsupported output_dtype"):
         call(output_dtype=3)
-    with pytest.raises(RuntimeError, match="INT8 output"):
+    # A:125-129: mixed tables fail the reference's own check, with its message
+    with pytest.raises(RuntimeError, match="int8 output_dtype requires all tables to use int8 weights"):
         call(output_dtype=2)
+    # all-INT8 tables pass it and meet the kernels' rejection (P:336-338)
+    m8 = IntNBitTableBatchedEmbeddingBagsCodegen([(10, 16, SparseType.INT8)], device=gpu, output_dtype=FP32)
+    with pytest.raises(RuntimeError, match="INT8 output_dtype is not supported"):
+        op(dev_weights=m8.weights_dev, uvm_weights=m8.weights_uvm, weights_placements=m8.weights_placements,
+           weights_offsets=m8.weights_offsets, weights_tys=m8.weights_tys, D_offsets=m8.D_offsets,
+           total_D=m8.total_D, max_int2_D=0, max_int4_D=0, max_int8_D=16, max_float16_D=0, max_float32_D=0,
+           indices=idx, offsets=off[:3], pooling_mode=0, indice_weights=None, output_dtype=2,
+           lxu_cache_weights=None, lxu_cache_locations=None, row_alignment=16, max_float8_D=0,
+           fp8_exponent_bits=-1, fp8_exponent_bias=-1)
     with pytest.raises(RuntimeError, match="Len mismatch"):
         call(indice_weights=torch.rand(3, device=gpu))
     with pytest.raises(RuntimeError, match="pooling mode"):
