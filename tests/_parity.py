@@ -140,3 +140,24 @@ def assert_bag_parity(gpu_out, prob, ref32, pooling_mode, output_dtype, label=""
             f"{label}: {int(bad.sum())}/{bad.size} elements out of tolerance; first at {tuple(i)}: "
             f"gpu={got[tuple(i)]!r} ref={ref32[tuple(i)]!r} lim={lim[tuple(i)]:.3e}")
     return float((err / np.maximum(lim, 1e-30)).max(initial=0.0))
+
+
+def ulp_stats(gpu_out: torch.Tensor, ref_out: np.ndarray, output_dtype: int):
+    """Distance between the GPU output and the oracle's output in units in the last place
+    of the output dtype (bit patterns mapped to a monotonic integer scale): returns
+    (max distance, fraction of elements bit-identical)."""
+    if output_dtype == 0:  # fp32
+        a = gpu_out.float().cpu().numpy().view(np.int32).astype(np.int64)
+        b = np.ascontiguousarray(ref_out, dtype=np.float32).view(np.int32).astype(np.int64)
+        sign = np.int64(1) << 31
+    else:                  # fp16 / bf16 bit patterns
+        a = gpu_out.cpu().view(torch.int16).numpy().astype(np.int64) & 0xFFFF
+        b = np.ascontiguousarray(ref_out).astype(np.int64) & 0xFFFF
+        a = np.where(a >= 0x8000, a - 0x10000, a)
+        b = np.where(b >= 0x8000, b - 0x10000, b)
+        sign = np.int64(1) << 15
+    # sign-magnitude -> ordered integers (+0 and -0 both map to 0)
+    ka = np.where(a < 0, -(a + sign), a)
+    kb = np.where(b < 0, -(b + sign), b)
+    d = np.abs(ka - kb)
+    return int(d.max(initial=0)), float((d == 0).mean()) if d.size else 1.0
