@@ -171,6 +171,82 @@ def bench_nobag(args, pkg, dev):
     print(json.dumps(out), flush=True)
 
 
+def calib_chunks(first, n: int):
+    """Per 64-lookup chunk c of lookups [64 c, 64 c + 64) (tbe_calib_gather's `chunk`
+    records): {table of lookup 64 c, the table after the first boundary inside the chunk,
+    the lane of that boundary (64: none), 1 if a further table starts inside the chunk}.
+    `first` [T + 1] holds every table's first lookup (first[T] = n); empty tables share
+    their first position with the next table."""
+    import torch
+    T = first.numel() - 1
+    starts = torch.arange(0, n, 64, device=first.device, dtype=torch.int64)
+    ta = (torch.searchsorted(first, starts, right=True) - 1).clamp_(0, T - 1)       # table of the first lookup
+    tb = (torch.searchsorted(first, starts + 63, right=True) - 1).clamp_(0, T - 1)  # table of the last one
+    split = torch.where(tb > ta, first[ta + 1] - starts, torch.full_like(starts, 64))
+    tnext = (torch.searchsorted(first, starts + split.clamp(max=63), right=True) - 1).clamp_(0, T - 1)
+    more = (tb > tnext).to(torch.int64)
+    second = torch.where(tb > ta, tnext, (ta + 1).clamp(max=T - 1))
+    return torch.stack([ta, second, split, more], 1).to(torch.int32).contiguous()
+
+
+def gather_calibration(wl, stream, timed, order, per_call_ms, alg):
+    """The same batches through libtbe_calib.so's tbe_calib_gather: every lookup's unpadded
+    row read (one row per lane, 16-byte loads, index order) and an output-sized buffer
+    written, with no arithmetic and no bag structure.  Its time is the practical floor of
+    the operator's memory work on this workload; `op_over_floor` is the operator's time
+    over it.  None when the library is not built, the tables' row sizes differ (config 3),
+    a row stride is not a multiple of 16 or a row is above 512 bytes."""
+    import ctypes
+    import torch
+    from fbgemm_ascend_amd.sparse_types import unpadded_row_bytes
+
+    path = os.path.join(ROOT, "fbgemm-ascend_amd", "libtbe_calib.so")
+    m = wl.module
+    sizes = {unpadded_row_bytes(ty, D) for (_, D, ty) in m.specs}
+    if (not os.path.exists(path) or len(sizes) != 1 or max(sizes) > 512
+            or any(int(st) % 16 or E >= 2 ** 32 for st, (E, _, _) in zip(m.row_strides, m.specs))):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.tbe_calib_gather.restype = ctypes.c_int
+    dev = wl.indices.device
+    T = len(m.specs)
+    B = wl.spec.B
+    import numpy as np
+    wo = m.weights_offsets.cpu().tolist()
+    desc = np.array([[wo[t] & 0xFFFFFFFF, wo[t] >> 32, int(m.row_strides[t]) | (unpadded_row_bytes(ty, D) << 16), E]
+                     for t, (E, D, ty) in enumerate(m.specs)], dtype=np.uint32)
+    desc = torch.from_numpy(desc.view(np.int32)).to(dev)
+    row_bytes = sizes.pop()
+    out_sz = {0: 4, 1: 2, 5: 2}[m.output_dtype]
+    out_units = B * m.total_D * out_sz // 8
+    out = torch.empty(max(1, out_units), dtype=torch.int64, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    firsts, chunks = [], []
+    for bt in wl.batches:
+        f = bt.offsets.to(torch.int64)[torch.arange(T + 1, device=dev) * B].contiguous()
+        firsts.append(f)
+        chunks.append(calib_chunks(f, bt.indices.numel()))
+    P = ctypes.c_void_p
+
+    def run(i):
+        bt = wl.batches[i]
+        rc = lib.tbe_calib_gather(P(m.weights_dev.data_ptr()), P(bt.indices.data_ptr()),
+                                  ctypes.c_int(bt.indices.element_size()), P(firsts[i].data_ptr()),
+                                  P(desc.data_ptr()), P(chunks[i].data_ptr()), ctypes.c_int32(row_bytes),
+                                  ctypes.c_int64(bt.indices.numel()), P(out.data_ptr()), ctypes.c_int64(out_units),
+                                  P(sink.data_ptr()), P(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"tbe_calib_gather failed ({rc})")
+
+    for i in range(len(wl.batches)):
+        run(i)
+    ms, _ = timed(order, fn=run)
+    floor_ms = sum(ms) / len(ms)
+    total_alg = sum(alg[i] for i in order)
+    return {"kernel_ms": floor_ms, "frac": total_alg / (sum(ms) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "op_over_floor": (sum(per_call_ms) / len(per_call_ms)) / floor_ms}
+
+
 def _cpu_threads():
     """Host threads of the CPU legs: the process's CPU affinity, capped by OMP_NUM_THREADS
     when it is set (the GPU boxes set it to their per-GPU CPU share)."""
@@ -444,14 +520,17 @@ def main():
     alg = [wl.algorithmic_bytes(i) for i in range(K)]
     stream = torch.cuda.current_stream(dev)
 
-    def timed(order):
+    def timed(order, fn=None):
         """HIP events around every call on the launch stream; returns (per-call ms, wall s)."""
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for (a, b), i in zip(evs, order):
             a.record(stream)
-            calls[i]()
+            if fn is None:
+                calls[i]()
+            else:
+                fn(i)
             b.record(stream)
         torch.cuda.synchronize()
         return [a.elapsed_time(b) for a, b in evs], time.perf_counter() - t0
@@ -490,6 +569,8 @@ def main():
         cold_ms = sum(c for c, _ in cold) / len(cold)
         cold_alg = sum(alg[i] for _, i in cold) / len(cold)
         del scrub
+
+    calib = gather_calibration(wl, stream, timed, order, per_call_ms, alg)
 
     traffic = None
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"tbe_cfg{args.config}_traffic.json")
@@ -532,6 +613,7 @@ def main():
         "replay_same_batch": ({"kernel_ms": replay_kernel_ms, "frac": frac(replay_kernel_ms, alg[0])}
                               if replay_kernel_ms is not None else None),
         "cold_cache": ({"kernel_ms": cold_ms, "frac": frac(cold_ms, cold_alg)} if cold_ms is not None else None),
+        "gather_calibration": calib,
     }
     res["cpu_baseline"], res["cpu_baseline_library"] = (None, None)
     if not args.no_cpu_baseline:
