@@ -158,6 +158,9 @@ def bench_nobag(args, pkg, dev):
     N = wl.num_indices
     nbytes = N * (68 + wl.indices.element_size() + 128 * 2)
     achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    # the same rows read and an [N, 128] fp16 output written, no arithmetic
+    calib = gather_calibration(wl, stream, lambda order, fn: time_calls(stream, order, fn), [0] * args.steps,
+                               [mean_ms], [nbytes], out_bytes=N * 128 * 2)
     out = {"metric": "TBE nobag lookups/s, 1 GPU", "value": N / (mean_ms * 1e-3), "unit": "lookups/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int4",
@@ -167,7 +170,7 @@ def bench_nobag(args, pkg, dev):
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
            "kernel_ms": mean_ms, "kernel_ms_median": ms[len(ms) // 2], "bytes_per_step": nbytes,
-           "cpu_baseline": None}
+           "gather_calibration": calib, "cpu_baseline": None}
     print(json.dumps(out), flush=True)
 
 
@@ -189,7 +192,21 @@ def calib_chunks(first, n: int):
     return torch.stack([ta, second, split, more], 1).to(torch.int32).contiguous()
 
 
-def gather_calibration(wl, stream, timed, order, per_call_ms, alg):
+def time_calls(stream, order, fn):
+    """HIP events around fn(i) for every i of `order` on `stream`; returns (per-call ms, wall s)."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for (a, b), i in zip(evs, order):
+        a.record(stream)
+        fn(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs], time.perf_counter() - t0
+
+
+def gather_calibration(wl, stream, timed, order, per_call_ms, alg, out_bytes=None):
     """The same batches through libtbe_calib.so's tbe_calib_gather: every lookup's unpadded
     row read (one row per lane, 16-byte loads, index order) and an output-sized buffer
     written, with no arithmetic and no bag structure.  Its time is the practical floor of
@@ -218,7 +235,7 @@ def gather_calibration(wl, stream, timed, order, per_call_ms, alg):
     desc = torch.from_numpy(desc.view(np.int32)).to(dev)
     row_bytes = sizes.pop()
     out_sz = {0: 4, 1: 2, 5: 2}[m.output_dtype]
-    out_units = B * m.total_D * out_sz // 8
+    out_units = (B * m.total_D * out_sz if out_bytes is None else out_bytes) // 8
     out = torch.empty(max(1, out_units), dtype=torch.int64, device=dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     firsts, chunks = [], []

@@ -5,8 +5,8 @@
 // structure: every lookup's unpadded row is read (one row per lane, 16-byte loads
 // covering the row's bytes, in index order, so the same 128-byte lines are fetched in
 // the same order as by the operator), and a buffer the size of the operator's output is
-// written, interleaved with the reads (lookup i writes 8-byte units i, i + n, ...) as the
-// operator's output stores are.  Its time is the practical floor of the operator on that
+// written, interleaved with the reads as the operator's output stores are (each lookup
+// writes its share of the output right after its row).  Its time is the practical floor of the operator on that
 // workload: what the memory system takes for the same lines with as many loads in flight
 // as the GPU holds.  Rows are read in 16-byte pieces from their start, so row strides must
 // be multiples of 16 (row_alignment 16, as in every benchmark configuration), and every
@@ -52,8 +52,17 @@ __global__ __launch_bounds__(256) void calib_gather_kernel(const uint8_t* __rest
 #pragma unroll
     for (int k = 0; k < KC; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
   }
-  // the output-sized write, in 8-byte units: lookup i writes units i, i + n, i + 2n, ...
-  for (int64_t u = i; u < out_units; u += n) out[u] = make_uint2(acc, static_cast<uint32_t>(u));
+  // the output-sized write, in 8-byte units: the wave's 64 lookups own units
+  // [k i0, k (i0 + 64)) with k = out_units / n (an output row per lookup when k is whole:
+  // nobag), written by the wave's lanes together, one coalesced store per 64 units; then
+  // units n k + i, n k + i + n, ... of the remainder (pooled outputs: about one unit per lookup)
+  const int64_t k = out_units / n;
+  const int64_t i0 = i & ~int64_t(63);
+  for (int64_t j = 0; j < k; ++j) {
+    const int64_t u = i0 * k + j * 64 + lane;
+    if (u < n * k) out[u] = make_uint2(acc, static_cast<uint32_t>(j));
+  }
+  for (int64_t u = n * k + i; u < out_units; u += n) out[u] = make_uint2(acc, static_cast<uint32_t>(u));
   if (acc == 0x9E3779B9u) sink[0] = acc;  // keeps the loads
 }
 
