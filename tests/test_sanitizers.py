@@ -37,7 +37,10 @@ def sanitized_env():
     if not shutil.which("hipcc") and not os.path.exists("/opt/rocm/bin/hipcc"):
         pytest.skip("hipcc not available")
     b = _build_module()
-    sources = [os.path.join(PKG, "csrc", s) for s in os.listdir(os.path.join(PKG, "csrc"))]
+    csrc = os.path.join(PKG, "csrc")
+    sources = [os.path.join(csrc, s) for s in b.HIP_SOURCES]
+    sources += [os.path.join(csrc, s) for s in os.listdir(csrc) if s.endswith(".h")]
+    sources += [os.path.join(ROOT, "include", s) for s in os.listdir(os.path.join(ROOT, "include"))]
     sources.append(os.path.join(ROOT, "oracle", "tbe_oracle.c"))
     newest = max(os.path.getmtime(s) for s in sources)
     if not all(os.path.exists(p) and os.path.getmtime(p) >= newest for p in (ASAN_LIB, ASAN_ORACLE)):
