@@ -8,6 +8,8 @@ random permutation per table), int32 indices/offsets, SUM pooling, fp16 output
 torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function over that batch,
 with every input resident in HBM before the timed region starts.
 
+Timing: one pair of HIP events on the launch stream around the timed calls (GPU time per
+call = span / calls) and the host wall clock around the same loop (`ms_per_step`).
 The timed loop rotates over --batches (default 4) distinct batches drawn from the
 same distributions (every table keeps its Zipf rank -> row map), all resident in
 HBM before timing, so each call meets the cache state a stream of fresh requests
@@ -160,7 +162,7 @@ def bench_nobag(args, pkg, dev):
     achieved = nbytes / (mean_ms * 1e-3) / 1e9
     # the same rows read and an [N, 128] fp16 output written, no arithmetic
     calib = gather_calibration(wl, stream, lambda order, fn: time_calls(stream, order, fn), [0] * args.steps,
-                               [mean_ms], [nbytes], out_bytes=N * 128 * 2)
+                               mean_ms, [nbytes], out_bytes=N * 128 * 2)
     out = {"metric": "TBE nobag lookups/s, 1 GPU", "value": N / (mean_ms * 1e-3), "unit": "lookups/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int4",
@@ -193,25 +195,28 @@ def calib_chunks(first, n: int):
 
 
 def time_calls(stream, order, fn):
-    """HIP events around fn(i) for every i of `order` on `stream`; returns (per-call ms, wall s)."""
+    """fn(i) for every i of `order` between one pair of HIP events on `stream`; returns
+    (GPU ms per call, wall s)."""
     import torch
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for (a, b), i in zip(evs, order):
-        a.record(stream)
+    a.record(stream)
+    for i in order:
         fn(i)
-        b.record(stream)
+    b.record(stream)
     torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs], time.perf_counter() - t0
+    return a.elapsed_time(b) / len(order), time.perf_counter() - t0
 
 
-def gather_calibration(wl, stream, timed, order, per_call_ms, alg, out_bytes=None):
+def gather_calibration(wl, stream, timed, order, op_ms, alg, out_bytes=None):
     """The same batches through libtbe_calib.so's tbe_calib_gather: every lookup's unpadded
     row read (one row per lane, 16-byte loads, index order) and an output-sized buffer
     written, with no arithmetic and no bag structure.  Its time is the practical floor of
     the operator's memory work on this workload; `op_over_floor` is the operator's time
-    over it.  None when the library is not built, the tables' row sizes differ (config 3),
+    over it (`timed(order, fn)` returns GPU ms per call and wall seconds; `op_ms` is the
+    operator's ms per call measured the same way).  None when the library is not built,
+    the tables' row sizes differ (config 3),
     a row stride is not a multiple of 16 or a row is above 512 bytes."""
     import ctypes
     import torch
@@ -257,11 +262,10 @@ def gather_calibration(wl, stream, timed, order, per_call_ms, alg, out_bytes=Non
 
     for i in range(len(wl.batches)):
         run(i)
-    ms, _ = timed(order, fn=run)
-    floor_ms = sum(ms) / len(ms)
+    floor_ms, _ = timed(order, fn=run)
     total_alg = sum(alg[i] for i in order)
-    return {"kernel_ms": floor_ms, "frac": total_alg / (sum(ms) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-            "op_over_floor": (sum(per_call_ms) / len(per_call_ms)) / floor_ms}
+    return {"kernel_ms": floor_ms, "frac": total_alg / (floor_ms * len(order) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "op_over_floor": op_ms / floor_ms}
 
 
 def _cpu_threads():
@@ -552,24 +556,41 @@ def main():
         torch.cuda.synchronize()
         return [a.elapsed_time(b) for a, b in evs], time.perf_counter() - t0
 
+    def timed_span(order, fn=None):
+        """One HIP event before and one after the calls, on the launch stream (no event
+        between calls, which would add its own gap to every call); returns (GPU ms per
+        call, wall s)."""
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        a.record(stream)
+        for i in order:
+            if fn is None:
+                calls[i]()
+            else:
+                fn(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / len(order), time.perf_counter() - t0
+
     for s in range(args.warmup):
         calls[s % K]()
     torch.cuda.synchronize()
 
     # headline: a stream of distinct batches from the same distributions (batch s % K)
     order = [s % K for s in range(args.steps)]
-    per_call_ms, wall = timed(order)
-    kernel_ms = sum(per_call_ms) / len(per_call_ms)
+    kernel_ms, wall = timed_span(order)
     ms_per_step = wall * 1e3 / args.steps
     total_lookups = sum(lookups[i] for i in order)
     total_alg = sum(alg[i] for i in order)
-    achieved = total_alg / (sum(per_call_ms) * 1e-3) / 1e9
+    achieved = total_alg / (kernel_ms * args.steps * 1e-3) / 1e9
+    # the same calls with an event pair around each one (per-call spread; each pair adds a gap)
+    per_call_ms, _ = timed(order)
 
     # the same batch replayed back to back (L2 and MALL hold the previous call's rows)
     replay_kernel_ms = None
     if not args.no_replay:
-        replay_ms, _ = timed([0] * args.steps)
-        replay_kernel_ms = sum(replay_ms) / len(replay_ms)
+        replay_kernel_ms, _ = timed_span([0] * args.steps)
 
     cold_ms = None
     if not args.no_cold:
@@ -587,7 +608,7 @@ def main():
         cold_alg = sum(alg[i] for _, i in cold) / len(cold)
         del scrub
 
-    calib = gather_calibration(wl, stream, timed, order, per_call_ms, alg)
+    calib = gather_calibration(wl, stream, timed_span, order, kernel_ms, alg)
 
     traffic = None
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"tbe_cfg{args.config}_traffic.json")
@@ -624,7 +645,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic},
         "kernel_ms": kernel_ms,
-        "kernel_ms_median": sorted(per_call_ms)[len(per_call_ms) // 2],
+        "kernel_ms_per_call_events": {"mean": sum(per_call_ms) / len(per_call_ms),
+                                      "median": sorted(per_call_ms)[len(per_call_ms) // 2]},
         "algorithmic_bytes_per_step": total_alg / args.steps,
         "bags_per_s": wl.num_bags * args.steps / wall,
         "replay_same_batch": ({"kernel_ms": replay_kernel_ms, "frac": frac(replay_kernel_ms, alg[0])}
