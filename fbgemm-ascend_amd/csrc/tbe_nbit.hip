@@ -347,6 +347,9 @@ int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_or
     if (bits == 0) return fail(TBE_ERR_UNSUPPORTED, "table %d: unsupported weight type %d", t, ty);
     const int64_t D = static_cast<int64_t>(in->D_offsets[t + 1]) - in->D_offsets[t];
     if (D < 0) return fail(TBE_ERR_INVALID_ARG, "D_offsets must be non-decreasing (table %d)", t);
+    // a zero-width table would have a zero row stride (FP rows) and no column to pool
+    if (D == 0) return fail(TBE_ERR_INVALID_ARG, "table %d: D must be positive (D_offsets[%d] == D_offsets[%d])", t,
+                            t, t + 1);
     if ((D * bits) % 32 != 0)
       return fail(TBE_ERR_UNSUPPORTED,
                   "table %d: D=%lld of weight type %d does not fill whole 4-byte words (D*bits %% 32 != 0)",

@@ -303,3 +303,75 @@ def test_calibration_chunk_records_find_every_lookups_table():
                 while f[t + 1] <= i:
                     t += 1
             assert t == truth, (i, t, truth, c[i >> 6], f)
+
+
+def test_plan_fuzz_accepts_or_rejects_cleanly(pkg):
+    """Random table metadata, valid layouts with one field broken half of the time
+    (unknown type, a width that does not fill 4-byte words, zero or decreasing
+    D_offsets, an offset outside the buffer or unaligned, an odd row alignment, FP8
+    parameters out of range): the planner either rejects with a message or returns a plan
+    whose every table lies inside dev_weights and whose groups list each table exactly
+    once.  (Run also under ASan and UBSan by test_sanitizers.py.)"""
+    import random
+    c = pkg.capi
+    rnd = random.Random(1234)
+    word_D = {FP32: 1, FP16: 2, BF16: 2, FP8: 4, INT8: 4, INT4: 8, INT2: 16}
+    accepted = rejected = 0
+    for _ in range(600):
+        T = rnd.choice([1, 2, 3, 7, 26, 64])
+        tys = [rnd.choice([FP32, FP16, INT8, INT4, INT2, BF16, FP8]) for _ in range(T)]
+        Ds = [word_D[ty] * rnd.choice([1, 2, 3, 8, 16, 32, 64, 65, 128, 300]) for ty in tys]
+        align = rnd.choice([4, 8, 16, 16, 32, 64])
+        rows = [rnd.choice([1, 2, 10, 1000]) for _ in range(T)]
+        woffs, pos = [], 0
+        for ty, D, E in zip(tys, Ds, rows):
+            woffs.append(pos)
+            pos += E * _stride(ty, D, align)
+        nbytes = pos + rnd.choice([0, 0, 4, 1000])
+        bits, bias = rnd.choice([(4, 7), (5, 15), (1, 0), (7, 120)])
+        dofs = [0] + np.cumsum(Ds).tolist()
+        if rnd.random() < 0.5:  # break one thing
+            k = rnd.randrange(T)
+            what = rnd.randrange(9)
+            if what == 0:
+                tys[k] = rnd.choice([7, 9, 255])
+            elif what == 1:
+                dofs[k + 1] = dofs[k] + rnd.choice([1, 3, 5])  # a width that does not fill words (or 0-width)
+                dofs[k + 2:] = [d - Ds[k] + dofs[k + 1] - dofs[k] for d in dofs[k + 2:]]
+            elif what == 2:
+                dofs[k + 1] = dofs[k]  # zero-width table
+            elif what == 3:
+                dofs[k + 1] = dofs[k] - 4  # decreasing
+            elif what == 4:
+                woffs[k] = rnd.choice([-16, nbytes + 16, 2 ** 62])
+            elif what == 5:
+                woffs[k] += 2  # unaligned
+            elif what == 6:
+                align = rnd.choice([0, -16, 6, 1, 1 << 20])
+            elif what == 7:
+                bits, bias = rnd.choice([(-1, -1), (0, 0), (8, 1), (3, -200), (7, 1000)])
+            else:
+                nbytes = rnd.choice([0, 16])
+        try:
+            descs, order, s = c.plan(woffs, tys, dofs, nbytes, align, bits, bias)
+        except c.TbeError as e:
+            assert str(e).strip(), "rejection without a message"
+            rejected += 1
+            continue
+        accepted += 1
+        seen = []
+        for gi in range(s.num_groups):
+            g = s.groups[gi]
+            seen += list(order[g.first:g.first + g.count])
+        assert sorted(seen) == list(range(T))
+        for t in range(T):
+            d = descs[t]
+            assert d.row_stride > 0 and d.num_rows >= 0
+            assert 0 <= d.weights_offset and d.weights_offset + d.num_rows * d.row_stride <= nbytes
+    assert accepted > 100 and rejected > 100, (accepted, rejected)
+
+
+def _stride(ty, D, align):
+    bits = {FP32: 32, FP16: 16, BF16: 16, FP8: 8, INT8: 8, INT4: 4, INT2: 2}[ty]
+    u = D * bits // 8 + (4 if ty in (INT8, INT4, INT2) else 0)
+    return (u + align - 1) // align * align
