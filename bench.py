@@ -67,7 +67,6 @@ def _parse():
 def bench_permute(args, pkg, dev):
     """permute_pooled_embs on the pooled output of config 4 ([32768, 200 x 128] fp16):
     a strided column copy, priced as 2 * B * total_D * 2 bytes per call."""
-    import numpy as np
     import torch
     import __graft_entry__ as graft
 
@@ -216,9 +215,10 @@ def gather_calibration(wl, stream, timed, order, op_ms, alg, out_bytes=None):
     the operator's memory work on this workload; `op_over_floor` is the operator's time
     over it (`timed(order, fn)` returns GPU ms per call and wall seconds; `op_ms` is the
     operator's ms per call measured the same way).  None when the library is not built,
-    the tables' row sizes differ (config 3),
-    a row stride is not a multiple of 16 or a row is above 512 bytes."""
+    the tables' row sizes differ (config 3), a row stride is not a multiple of 16 or a
+    row is above 512 bytes."""
     import ctypes
+    import numpy as np
     import torch
     from fbgemm_ascend_amd.sparse_types import unpadded_row_bytes
 
@@ -233,7 +233,6 @@ def gather_calibration(wl, stream, timed, order, op_ms, alg, out_bytes=None):
     dev = wl.indices.device
     T = len(m.specs)
     B = wl.spec.B
-    import numpy as np
     wo = m.weights_offsets.cpu().tolist()
     desc = np.array([[wo[t] & 0xFFFFFFFF, wo[t] >> 32, int(m.row_strides[t]) | (unpadded_row_bytes(ty, D) << 16), E]
                      for t, (E, D, ty) in enumerate(m.specs)], dtype=np.uint32)
@@ -322,7 +321,6 @@ def _sample_bags(wl, nsamp):
 def cpu_baseline(wl, target_s: float):
     """Time the C oracle (OpenMP) on a bounded sample of the workload: the first B/8 samples
     of every table, reading rows from a host copy of the whole dev_weights buffer."""
-    import numpy as np
     import torch
     import __graft_entry__ as graft
 
@@ -343,8 +341,6 @@ def cpu_baseline(wl, target_s: float):
     else:
         sys.path.insert(0, os.path.join(ROOT, "tests"))
         from _parity import compact_problem
-        g = torch.Generator(device=wl.indices.device)
-        g.manual_seed(17)
         b_sel = torch.arange(nsamp, device=wl.indices.device)
         prob = compact_problem(m, wl.indices, wl.offsets, wl.per_sample_weights, b_sel)
         layout = "compacted: only the sample's referenced rows copied to host (tables exceed host copy limit)"
@@ -435,7 +431,6 @@ def library_baseline(wl, prob, cores: int, target_s: float):
 def bench_bucketize(args, pkg, dev):
     """block_bucketize_sparse_features on the reference's i64_stress perf case, priced at the
     op's unavoidable bytes: indices read once and written once, lengths read, new_lengths written."""
-    import numpy as np
     import torch
     import __graft_entry__ as graft
 
