@@ -1,4 +1,5 @@
-"""The operators under HIP graph capture (torch.cuda.CUDAGraph).
+"""The operators under HIP graph capture (torch.cuda.CUDAGraph), and the TBE forward
+called concurrently from several caller streams and host threads.
 
 A serving loop captures the lookup once and replays it; the TBE forward forks its
 table groups onto library streams and joins them back with events, which must come
@@ -120,3 +121,48 @@ def test_permute_pooled_embs_graph_replays(pkg, gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, want), f"replay {rep}"
+
+
+def test_concurrent_caller_streams_and_threads(pkg, gpu):
+    """Two modules of different layouts called alternately on two caller streams, and from
+    two host threads: each caller stream gets its own library streams and each layout its
+    own cached plan, so every output equals the same call made alone."""
+    import threading
+    ma = _mixed_module(pkg, gpu, 0, FP16, seed=21)
+    mb = _mixed_module(pkg, gpu, 1, FP32, seed=22)
+    ia, oa, pa = _inputs(ma, gpu, 80, 3, False)
+    ib, ob, pb = _inputs(mb, gpu, 80, 4, True)
+    want_a = ma(ia, oa, pa)
+    want_b = mb(ib, ob, pb)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    outs_a, outs_b = [], []
+    for _ in range(8):  # interleaved enqueue on two streams
+        with torch.cuda.stream(sa):
+            outs_a.append(ma(ia, oa, pa))
+        with torch.cuda.stream(sb):
+            outs_b.append(mb(ib, ob, pb))
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, want_a) for o in outs_a)
+    assert all(torch.equal(o, want_b) for o in outs_b)
+
+    errors = []
+
+    def worker(m, idx, off, psw, want, n):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                got = [m(idx, off, psw) for _ in range(n)]
+            s.synchronize()
+            if not all(torch.equal(o, want) for o in got):
+                errors.append("mismatch")
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=worker, args=(ma, ia, oa, pa, want_a, 10)),
+          threading.Thread(target=worker, args=(mb, ib, ob, pb, want_b, 10))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=120)
+    assert not errors, errors
