@@ -166,8 +166,12 @@ typedef struct TbeNbitArgs {
 /*
  * Validate the table metadata and fill descs[T], table_order[T] (host memory)
  * and *summary (which lists the table groups the forward launches one kernel
- * for).  Mirrors the shape checks of H:95-204 and A:116-151.  Returns TBE_OK or
- * a negative TbeStatus; tbe_last_error() then names the failed check.
+ * for).  Mirrors the shape checks of H:95-204 and A:116-151, and rejects what the
+ * kernels cannot address: a known weight type per table, D_offsets increasing
+ * (every table at least one column), rows of whole 4-byte words, 4-byte aligned
+ * table offsets inside dev_weights, row_alignment a positive multiple of 4, and
+ * FP8 exponent bits / bias in range when an FP8 table is present.  Returns TBE_OK
+ * or a negative TbeStatus; tbe_last_error() then names the failed check.
  */
 int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_order,
                   TbePlanSummary* summary);
