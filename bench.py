@@ -267,6 +267,39 @@ def gather_calibration(wl, stream, timed, order, op_ms, alg, out_bytes=None):
             "op_over_floor": op_ms / floor_ms}
 
 
+def graph_replay(calls, K: int, stream, per_graph: int = 20, replays: int = 10):
+    """The op captured in a HIP graph (torch.cuda.CUDAGraph): `per_graph` calls rotating the
+    K batches, warmed up eagerly on the capture stream first, then replayed; GPU ms per call
+    between one event pair around the replays.  Launch-bound configurations (config 0) show
+    what graph replay saves per call.  None if the capture fails."""
+    import torch
+    cap = torch.cuda.Stream()
+    cap.wait_stream(stream)
+    try:
+        with torch.cuda.stream(cap):
+            for i in range(per_graph):
+                calls[i % K]()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(per_graph):
+                calls[i % K]()
+        torch.cuda.synchronize()
+    except RuntimeError as e:
+        return {"error": str(e)[:200]}
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(replays):
+        g.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / (replays * per_graph)
+    del g
+    return {"ms_per_call": ms, "calls_per_graph": per_graph}
+
+
 def _cpu_threads():
     """Host threads of the CPU legs: the process's CPU affinity, capped by OMP_NUM_THREADS
     when it is set (the GPU boxes set it to their per-GPU CPU share)."""
@@ -604,6 +637,7 @@ def main():
         del scrub
 
     calib = gather_calibration(wl, stream, timed_span, order, kernel_ms, alg)
+    graph = None if args.flags else graph_replay(calls, K, stream)
 
     traffic = None
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"tbe_cfg{args.config}_traffic.json")
@@ -648,6 +682,7 @@ def main():
                               if replay_kernel_ms is not None else None),
         "cold_cache": ({"kernel_ms": cold_ms, "frac": frac(cold_ms, cold_alg)} if cold_ms is not None else None),
         "gather_calibration": calib,
+        "graph_replay": graph,
     }
     res["cpu_baseline"], res["cpu_baseline_library"] = (None, None)
     if not args.no_cpu_baseline:
