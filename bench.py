@@ -352,8 +352,9 @@ def _sample_bags(wl, nsamp):
 
 
 def cpu_baseline(wl, target_s: float):
-    """Time the C oracle (OpenMP) on a bounded sample of the workload: the first B/8 samples
-    of every table, reading rows from a host copy of the whole dev_weights buffer."""
+    """Time the C oracle (OpenMP) on a bounded sample of the workload: the whole batch when it
+    holds at most 2 M lookups, else the first B/8 samples of every table, reading rows from
+    a host copy of the whole dev_weights buffer."""
     import torch
     import __graft_entry__ as graft
 
@@ -361,7 +362,8 @@ def cpu_baseline(wl, target_s: float):
     cores = _cpu_threads()
     m = wl.module
     B = wl.spec.B
-    nsamp = max(1, B // 8)
+    # the whole batch when it is small (per-call overheads would dominate a slice of it)
+    nsamp = B if wl.num_indices <= (2 << 20) else max(1, B // 8)
     pm = int(m.pooling_mode)
     bits, bias = m.fp8_exponent_bits, m.fp8_exponent_bias
     if m.weights_dev.numel() <= _HOST_TABLE_LIMIT:
