@@ -324,16 +324,17 @@ def _cpu_model():
     return "unknown"
 
 
-# host copies of the tables above this size are not made; the CPU legs then run on
-# the referenced rows only (and say so)
+# tables up to this size are copied to the host whole; beyond it the CPU legs take the
+# first tables that fit in _HOST_SUBSET_BYTES (config 4: 10 of its 200 tables) and say so
 _HOST_TABLE_LIMIT = 32 << 30
+_HOST_SUBSET_BYTES = 8 << 30
 
 
-def _sample_bags(wl, nsamp):
-    """Indices/offsets/weights of the first `nsamp` samples of every table (host arrays,
-    original row ids), in the op's table-major bag order."""
+def _sample_bags(wl, nsamp, k=None):
+    """Indices/offsets/weights of the first `nsamp` samples of each of the first k tables (all
+    by default; host arrays, original row ids), in the op's table-major bag order."""
     import numpy as np
-    T = len(wl.module.specs)
+    T = len(wl.module.specs) if k is None else k
     B = wl.spec.B
     off = wl.offsets.cpu().numpy().astype(np.int64)
     idx = wl.indices.cpu().numpy()
@@ -354,31 +355,30 @@ def _sample_bags(wl, nsamp):
 def cpu_baseline(wl, target_s: float):
     """Time the C oracle (OpenMP) on a bounded sample of the workload: the whole batch when it
     holds at most 2 M lookups, else the first B/8 samples of every table, reading rows from
-    a host copy of the whole dev_weights buffer."""
-    import torch
+    a host copy of the whole tables (of the first tables that fit in _HOST_SUBSET_BYTES when
+    all of them exceed _HOST_TABLE_LIMIT: config 4, labelled as a subset)."""
+    import numpy as np
     import __graft_entry__ as graft
 
     oracle = graft.load_oracle()
     cores = _cpu_threads()
     m = wl.module
     B = wl.spec.B
+    T = len(m.specs)
     # the whole batch when it is small (per-call overheads would dominate a slice of it)
     nsamp = B if wl.num_indices <= (2 << 20) else max(1, B // 8)
     pm = int(m.pooling_mode)
     bits, bias = m.fp8_exponent_bits, m.fp8_exponent_bias
-    if m.weights_dev.numel() <= _HOST_TABLE_LIMIT:
-        weights = m.weights_dev.cpu().numpy()
-        s_idx, s_off, s_psw = _sample_bags(wl, nsamp)
-        prob = dict(weights=weights, weights_offsets=m.weights_offsets.cpu().numpy(),
-                    weights_tys=m.weights_tys.cpu().numpy(), D_offsets=m.D_offsets.cpu().numpy(),
-                    indices=s_idx, offsets=s_off, psw=s_psw)
-        layout = "whole tables in host memory"
-    else:
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
-        from _parity import compact_problem
-        b_sel = torch.arange(nsamp, device=wl.indices.device)
-        prob = compact_problem(m, wl.indices, wl.offsets, wl.per_sample_weights, b_sel)
-        layout = "compacted: only the sample's referenced rows copied to host (tables exceed host copy limit)"
+    wo = m.weights_offsets.cpu().numpy()
+    ends = wo + np.array([E * int(st) for (E, _, _), st in zip(m.specs, m.row_strides)], dtype=np.int64)
+    # tables are laid out in order: keep the first k whose rows end within the host copy limit
+    k = T if int(ends.max()) <= _HOST_TABLE_LIMIT else max(1, int(np.searchsorted(ends, _HOST_SUBSET_BYTES, "right")))
+    weights = m.weights_dev[:int(ends[:k].max())].cpu().numpy()
+    s_idx, s_off, s_psw = _sample_bags(wl, nsamp, k)
+    prob = dict(weights=weights, weights_offsets=wo[:k], weights_tys=m.weights_tys.cpu().numpy()[:k],
+                D_offsets=m.D_offsets.cpu().numpy()[:k + 1], indices=s_idx, offsets=s_off, psw=s_psw)
+    layout = ("whole tables in host memory" if k == T else
+              f"first {k} of {T} tables (whole, host-resident; all {T} exceed the host copy limit)")
     n_lookups = int(prob["offsets"][-1])
 
     def run():
@@ -395,38 +395,40 @@ def cpu_baseline(wl, target_s: float):
         if el >= target_s or reps >= 100000:
             break
     res = {"value": n_lookups * reps / el, "unit": "pooled lookups/s", "cores": cores, "kind": "port",
-           "sample": f"first {nsamp} of {B} samples x {len(m.specs)} tables ({n_lookups} lookups), {layout}, "
+           "sample": f"first {nsamp} of {B} samples x {k} tables ({n_lookups} lookups), {layout}, "
                      f"{reps} reps in {el:.1f}s, oracle/tbe_oracle.c OpenMP fp32 on {cores} threads "
                      f"(process affinity capped by OMP_NUM_THREADS, the box's per-GPU CPU share)",
            "cpu_model": _cpu_model()}
-    lib = library_baseline(wl, prob, cores, target_s) if layout.startswith("whole") else None
-    return res, lib
+    return res, library_baseline(wl, prob, k, cores, target_s)
 
 
-def library_baseline(wl, prob, cores: int, target_s: float):
-    """torch.ops.quantized.embedding_bag_{byte,4bit}_rowwise_offsets (FBGEMM's CPU kernels
-    shipped with torch), one call per table, on the same sample and whole tables repacked to
-    the scale/bias-last row layout those kernels read.  Unweighted SUM over uniform INT8/INT4
-    tables only; returns None otherwise.  Its output is fp32 (no fp16 cast)."""
+def library_baseline(wl, prob, k: int, cores: int, target_s: float):
+    """torch.ops.quantized.embedding_bag_{byte,4bit,2bit}_rowwise_offsets (FBGEMM's CPU kernels
+    shipped with torch), one call per INT8/INT4/INT2 table of the oracle's sample (the first k
+    tables), whole tables repacked to the scale/bias-last row layout those kernels read, with
+    the per-sample weights when the workload has them.  Tables of other row types are left
+    out (and counted out of the lookups); None if there is no INT table.  Those kernels sum
+    (MEAN is the same sum, scaled afterwards) and return fp32."""
     import numpy as np
     import torch
 
     m = wl.module
-    tys = {int(ty) for (_, _, ty) in m.specs}
-    if len(tys) != 1 or tys.pop() not in (2, 3) or wl.per_sample_weights is not None or int(m.pooling_mode) != 0:
-        return None
-    ty = int(m.specs[0][2])
-    fn = (torch.ops.quantized.embedding_bag_byte_rowwise_offsets if ty == 2
-          else torch.ops.quantized.embedding_bag_4bit_rowwise_offsets)
+    fns = {2: torch.ops.quantized.embedding_bag_byte_rowwise_offsets,
+           3: torch.ops.quantized.embedding_bag_4bit_rowwise_offsets,
+           4: torch.ops.quantized.embedding_bag_2bit_rowwise_offsets}
     w = prob["weights"]
     wo = prob["weights_offsets"]
-    T = len(m.specs)
-    Bs = (len(prob["offsets"]) - 1) // T
+    Bs = (len(prob["offsets"]) - 1) // k
     off = prob["offsets"].astype(np.int64)
     idx = prob["indices"].astype(np.int64)
-    tables, calls = [], []
-    for t, (E, D, _) in enumerate(m.specs):
-        payload = D if ty == 2 else D // 2
+    psw = prob["psw"]
+    calls, n_lookups, used = [], 0, set()
+    for t in range(k):
+        E, D, ty = m.specs[t]
+        ty = int(ty)
+        if ty not in fns:
+            continue
+        payload = D * {2: 8, 3: 4, 4: 2}[ty] // 8
         stride = int(m.row_strides[t])
         rows = w[wo[t]:wo[t] + E * stride].reshape(E, stride)
         if ty == 2:  # fp32 scale and bias after the codes
@@ -436,16 +438,20 @@ def library_baseline(wl, prob, cores: int, target_s: float):
             lib = np.concatenate([rows[:, 4:4 + payload], sb.view(np.uint8).reshape(E, 8)], 1)
         else:        # fp16 scale and bias after the codes
             lib = np.concatenate([rows[:, 4:4 + payload], rows[:, 0:4]], 1)
-        tables.append(torch.from_numpy(np.ascontiguousarray(lib)))
         lo, hi = off[t * Bs], off[(t + 1) * Bs]
-        calls.append((torch.from_numpy(idx[lo:hi]), torch.from_numpy(off[t * Bs:(t + 1) * Bs + 1] - lo)))
-    n_lookups = int(off[-1] - off[0])
+        pw = torch.from_numpy(np.ascontiguousarray(psw[lo:hi])) if psw is not None else None
+        calls.append((fns[ty], torch.from_numpy(np.ascontiguousarray(lib)), torch.from_numpy(idx[lo:hi]),
+                      torch.from_numpy(off[t * Bs:(t + 1) * Bs + 1] - lo), pw))
+        n_lookups += int(hi - lo)
+        used.add({2: "byte", 3: "4bit", 4: "2bit"}[ty])
+    if not calls:
+        return None
     prev = torch.get_num_threads()
     torch.set_num_threads(cores)
     try:
         def run():
-            for tab, (i, o) in zip(tables, calls):
-                fn(tab, i, o, False, 0, False, None, None, True)
+            for fn, tab, i, o, pw in calls:
+                fn(tab, i, o, False, 0, False, pw, None, True)
         run()
         reps, t0 = 0, time.perf_counter()
         while True:
@@ -456,10 +462,14 @@ def library_baseline(wl, prob, cores: int, target_s: float):
                 break
     finally:
         torch.set_num_threads(prev)
+    left_out = k - len(calls)
     return {"value": n_lookups * reps / el, "unit": "pooled lookups/s", "cores": cores, "kind": "library",
-            "sample": f"same sample as cpu_baseline ({n_lookups} lookups), whole tables repacked, "
-                      f"torch.ops.quantized.embedding_bag_{'byte' if ty == 2 else '4bit'}_rowwise_offsets "
-                      f"per table, fp32 out, {reps} reps in {el:.1f}s, torch.set_num_threads({cores})",
+            "sample": f"the oracle's sample, {len(calls)} INT tables ({n_lookups} lookups"
+                      + (f"; {left_out} tables of other row types left out" if left_out else "")
+                      + f"), whole tables repacked, torch.ops.quantized.embedding_bag_"
+                      f"{'/'.join(sorted(used))}_rowwise_offsets per table"
+                      + (" with per-sample weights" if psw is not None else "")
+                      + f", fp32 out, {reps} reps in {el:.1f}s, torch.set_num_threads({cores})",
             "cpu_model": _cpu_model()}
 
 
