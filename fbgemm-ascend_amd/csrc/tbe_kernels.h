@@ -830,6 +830,7 @@ __device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDes
 // What a lane needs to gather rows of one bag's table.
 struct BagCtx {
   __amdgpu_buffer_rsrc_t rs;  // the table's rows; range = rows * stride bytes
+  const uint8_t* tbase;       // row 0 (64-bit addressing)
   TbeTableDesc td;
   uint32_t col;               // byte offset of this lane's payload word in a row
   int dw;                     // payload word of this lane
@@ -848,16 +849,30 @@ __device__ __forceinline__ BagCtx bag_ctx(const KParams& p, const StagedBag& sb)
                                            static_cast<int>(static_cast<uint32_t>(c.td.num_rows) *
                                                             static_cast<uint32_t>(c.td.row_stride)),
                                            kRsrcWord3);
+  c.tbase = p.weights + c.td.weights_offset;
   return c;
 }
 
 // This lane's index of a chunk as a byte offset into the table (kNoRow for a
-// rejected index or a lane past the chunk's n indices).
+// rejected index or a lane past the chunk's n indices).  A64 (tables past 32-bit
+// byte offsets, fewer than 2^32 - 1 rows): the row index itself, kNoRow64 for none.
+constexpr uint32_t kNoRow64 = 0xFFFFFFFFu;
+template <bool A64 = false>
 __device__ __forceinline__ uint32_t row_offset(const BagCtx& c, uint64_t idx, int n) {
   const int lane = threadIdx.x & (kWave - 1);
-  const uint32_t rows = static_cast<uint32_t>(c.td.num_rows);
-  return (lane < n && idx < rows) ? static_cast<uint32_t>(idx) * static_cast<uint32_t>(c.td.row_stride) : kNoRow;
+  if constexpr (A64) {
+    return (lane < n && idx < static_cast<uint64_t>(c.td.num_rows)) ? static_cast<uint32_t>(idx) : kNoRow64;
+  } else {
+    const uint32_t rows = static_cast<uint32_t>(c.td.num_rows);
+    return (lane < n && idx < rows) ? static_cast<uint32_t>(idx) * static_cast<uint32_t>(c.td.row_stride) : kNoRow;
+  }
 }
+
+// Zeros that a lane without a row reads in its place under 64-bit addressing (no
+// range check there): a zero header and zero words add nothing.  Covers every
+// column offset a lane of a row reads (255 tiles of 64 words after the header).
+constexpr int kZeroRowWords = 256 * kWave + 4;
+static __device__ __align__(16) const uint32_t g_zero_row[kZeroRowWords] = {};
 
 // VW consecutive words at byte offset `off` of a buffer.
 template <int VW>
@@ -888,7 +903,7 @@ struct StepRegs {
 // Issue the loads of step `st` of a chunk (rows st*R*U .. st*R*U + R*U - 1).
 // Slot st*R*U + u*R + slot < 64 because R*U divides 64; slots past the chunk
 // read lanes that hold kNoRow and load zero.
-template <int WT, int LG, bool WEIGHTED, int VW>
+template <int WT, int LG, bool WEIGHTED, int VW, bool A64 = false>
 __device__ __forceinline__ void issue_step(const BagCtx& c, uint32_t my_off, float my_w, int st,
                                            StepRegs<unroll_for<LG, VW>(), VW>& r) {
   constexpr int R = kWave >> LG;
@@ -898,9 +913,21 @@ __device__ __forceinline__ void issue_step(const BagCtx& c, uint32_t my_off, flo
   for (int u = 0; u < U; ++u) {
     const int src = (st * R * U + u * R) * 4 + slot4;
     const uint32_t off = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(my_off)));
-    load_words<VW>(c.rs, off + c.col, r.d[u]);
-    if constexpr (Traits<WT>::kHdr) r.h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(c.rs, static_cast<int>(off), 0, 0));
-    else r.h[u] = 0u;
+    if constexpr (A64) {
+      static_assert(VW == 1, "64-bit addressing: one word per lane");
+      // off is a row index; a lane without a row reads the zero row (the address
+      // is selected, not the loaded value, so no wait is forced here)
+      const uint8_t* zero = reinterpret_cast<const uint8_t*>(g_zero_row);
+      const uint8_t* rp = off != kNoRow64 ? c.tbase + static_cast<uint64_t>(off) * static_cast<uint32_t>(c.td.row_stride)
+                                          : zero;
+      r.d[u][0] = load_word(rp + c.col);
+      if constexpr (Traits<WT>::kHdr) r.h[u] = load_word(rp);
+      else r.h[u] = 0u;
+    } else {
+      load_words<VW>(c.rs, off + c.col, r.d[u]);
+      if constexpr (Traits<WT>::kHdr) r.h[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(c.rs, static_cast<int>(off), 0, 0));
+      else r.h[u] = 0u;
+    }
     if constexpr (WEIGHTED) r.w[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(my_w)));
     else r.w[u] = 1.f;
   }
@@ -934,7 +961,7 @@ __device__ __forceinline__ void consume_step(const KParams& p, const StepRegs<un
 }
 
 // Steps st0.. of one chunk of <= 64 indices, each issued then consumed.
-template <int WT, int LG, bool WEIGHTED, int VW>
+template <int WT, int LG, bool WEIGHTED, int VW, bool A64>
 __device__ __forceinline__ void pool_steps(const KParams& p, const BagCtx& c, uint32_t my_off, float my_w, int n,
                                            int st0, float (&acc)[Traits<WT>::kEpd * VW], float& bacc) {
   constexpr int kSteps = kWave / ((kWave >> LG) * unroll_for<LG, VW>());
@@ -942,7 +969,7 @@ __device__ __forceinline__ void pool_steps(const KParams& p, const BagCtx& c, ui
   for (int st = 1; st < kSteps; ++st) {
     if (st >= st0 && st * (kWave / kSteps) < n) {  // wave-uniform
       StepRegs<unroll_for<LG, VW>(), VW> r;
-      issue_step<WT, LG, WEIGHTED, VW>(c, my_off, my_w, st, r);
+      issue_step<WT, LG, WEIGHTED, VW, A64>(c, my_off, my_w, st, r);
       // keep the step's loads together, ahead of the guarded accumulations
       __builtin_amdgcn_sched_barrier(0);
       consume_step<WT, LG, WEIGHTED, VW>(p, r, st, n, acc, bacc);
@@ -953,7 +980,7 @@ __device__ __forceinline__ void pool_steps(const KParams& p, const BagCtx& c, ui
 // Finish a bag whose step 0 rows are in `r0`: consume them, gather the rest of
 // the bag (longer than one step or one chunk), reduce and store (P:44-85 bag
 // walk, P:282-315 pooling, P:346-394 chunked bag, P:319-342 store).
-template <int WT, int LG, typename IndexT, bool WEIGHTED, int VW>
+template <int WT, int LG, typename IndexT, bool WEIGHTED, int VW, bool A64>
 __device__ __forceinline__ void finish_bag_fast(const KParams& p, const StagedBag& sb, const BagCtx& c,
                                                 uint32_t my_off, const StepRegs<unroll_for<LG, VW>(), VW>& r0) {
   constexpr int E = Traits<WT>::kEpd * VW;
@@ -964,17 +991,17 @@ __device__ __forceinline__ void finish_bag_fast(const KParams& p, const StagedBa
   const int L = sb.L;
   const int n0 = min(L, kWave);
   consume_step<WT, LG, WEIGHTED, VW>(p, r0, 0, n0, acc, bacc);
-  pool_steps<WT, LG, WEIGHTED, VW>(p, c, my_off, sb.w, n0, 1, acc, bacc);
+  pool_steps<WT, LG, WEIGHTED, VW, A64>(p, c, my_off, sb.w, n0, 1, acc, bacc);
   for (int base = kWave; base < L; base += kWave) {
     const int n = min(kWave, L - base);
     const uint64_t idx = load_index_chunk<IndexT>(p, sb.start + base, n);
     const float w = WEIGHTED ? load_weight_chunk(p, sb.start + base, n) : 0.f;
-    const uint32_t off = row_offset(c, idx, n);
+    const uint32_t off = row_offset<A64>(c, idx, n);
     StepRegs<unroll_for<LG, VW>(), VW> r;
-    issue_step<WT, LG, WEIGHTED, VW>(c, off, w, 0, r);
+    issue_step<WT, LG, WEIGHTED, VW, A64>(c, off, w, 0, r);
     __builtin_amdgcn_sched_barrier(0);
     consume_step<WT, LG, WEIGHTED, VW>(p, r, 0, n, acc, bacc);
-    pool_steps<WT, LG, WEIGHTED, VW>(p, c, off, w, n, 1, acc, bacc);
+    pool_steps<WT, LG, WEIGHTED, VW, A64>(p, c, off, w, n, 1, acc, bacc);
   }
   if (sb.valid) reduce_store<WT, LG, E>(p, c.td, L, c.dw, c.col_ok, sb.b, acc, bacc);
 }
@@ -1465,11 +1492,13 @@ __global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
 // ---------------------------------------------------------------- pooled kernels
 
 
-// Kernel for one group of 32-bit tables with weight type WT and 2^LG lanes per row.
+// Kernel for one group of tables with weight type WT and 2^LG lanes per row, rows
+// read with range-checked buffer loads at 32-bit byte offsets, or (A64, tables
+// past 4 GiB) with 64-bit addresses, a lane without a row reading the zero row.
 // Software pipeline over the wave's items: while bag i is consumed, the rows of
 // bag i+1 are in flight and the index chunk of bag i+2 is being fetched.  The
 // loop body is unrolled twice so the two row buffers swap roles without copies.
-template <int WT, int LG, typename IndexT, bool WEIGHTED, int VW>
+template <int WT, int LG, typename IndexT, bool WEIGHTED, int VW, bool A64 = false>
 __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
   // VW words per lane: 2^LGE lanes cover a row's 2^LG words of this column tile
   constexpr int LGE = VW == 2 ? LG - 1 : LG;
@@ -1482,16 +1511,16 @@ __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
   StagedBag s0 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, 0);
   StagedBag s1 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, 1);
   BagCtx c0 = bag_ctx<LGE, VW>(p, s0);
-  uint32_t off0 = row_offset(c0, s0.idx, min(s0.L, kWave));
+  uint32_t off0 = row_offset<A64>(c0, s0.idx, min(s0.L, kWave));
   StepRegs<U, VW> ra, rb;
-  issue_step<WT, LGE, WEIGHTED, VW>(c0, off0, s0.w, 0, ra);
+  issue_step<WT, LGE, WEIGHTED, VW, A64>(c0, off0, s0.w, 0, ra);
   while (true) {
     StagedBag s2 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, g + 2);
     BagCtx c1 = bag_ctx<LGE, VW>(p, s1);
-    uint32_t off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
-    issue_step<WT, LGE, WEIGHTED, VW>(c1, off1, s1.w, 0, rb);
+    uint32_t off1 = row_offset<A64>(c1, s1.idx, min(s1.L, kWave));
+    issue_step<WT, LGE, WEIGHTED, VW, A64>(c1, off1, s1.w, 0, rb);
     __builtin_amdgcn_sched_barrier(0);
-    finish_bag_fast<WT, LGE, IndexT, WEIGHTED, VW>(p, s0, c0, off0, ra);
+    finish_bag_fast<WT, LGE, IndexT, WEIGHTED, VW, A64>(p, s0, c0, off0, ra);
     if (++g >= nitems) break;
     s0 = s1;
     c0 = c1;
@@ -1500,10 +1529,10 @@ __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
 
     s2 = stage_bag<IndexT, WEIGHTED>(p, w, nitems, tab, g + 2);
     c1 = bag_ctx<LGE, VW>(p, s1);
-    off1 = row_offset(c1, s1.idx, min(s1.L, kWave));
-    issue_step<WT, LGE, WEIGHTED, VW>(c1, off1, s1.w, 0, ra);
+    off1 = row_offset<A64>(c1, s1.idx, min(s1.L, kWave));
+    issue_step<WT, LGE, WEIGHTED, VW, A64>(c1, off1, s1.w, 0, ra);
     __builtin_amdgcn_sched_barrier(0);
-    finish_bag_fast<WT, LGE, IndexT, WEIGHTED, VW>(p, s0, c0, off0, rb);
+    finish_bag_fast<WT, LGE, IndexT, WEIGHTED, VW, A64>(p, s0, c0, off0, rb);
     if (++g >= nitems) break;
     s0 = s1;
     c0 = c1;
@@ -1552,6 +1581,28 @@ KernelFn fast_kernel_for(bool index64, bool weighted, bool wide_words) {
     if (wide_words) return fast_kernel_vw<WT, LG, 2>(index64, weighted);
   }
   return fast_kernel_vw<WT, LG, 1>(index64, weighted);
+}
+
+// The per-bag kernel with 64-bit row addresses (one word per lane), for tables
+// past 32-bit byte offsets that still have fewer than 2^32 - 1 rows.
+template <int WT, int LG>
+KernelFn fast_kernel_a64_for(bool index64, bool weighted) {
+  if (index64)
+    return weighted ? pooled_fast_kernel<WT, LG, int64_t, true, 1, true> : pooled_fast_kernel<WT, LG, int64_t, false, 1, true>;
+  return weighted ? pooled_fast_kernel<WT, LG, int32_t, true, 1, true> : pooled_fast_kernel<WT, LG, int32_t, false, 1, true>;
+}
+
+template <int WT>
+KernelFn fast_kernel_a64_lg(int lg, bool index64, bool weighted) {
+  switch (lg) {
+    case 0: return fast_kernel_a64_for<WT, 0>(index64, weighted);
+    case 1: return fast_kernel_a64_for<WT, 1>(index64, weighted);
+    case 2: return fast_kernel_a64_for<WT, 2>(index64, weighted);
+    case 3: return fast_kernel_a64_for<WT, 3>(index64, weighted);
+    case 4: return fast_kernel_a64_for<WT, 4>(index64, weighted);
+    case 5: return fast_kernel_a64_for<WT, 5>(index64, weighted);
+    default: return fast_kernel_a64_for<WT, 6>(index64, weighted);
+  }
 }
 
 // wide_words: every table of the group has an even number of payload words

@@ -17,24 +17,31 @@ namespace tbe {
 
 // instantiated once, in tbe_kern_<type>.hip
 extern template KernelFn fast_kernel_lg<TBE_TY_FP32>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_FP32>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP32>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_FP32>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_FP16>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_FP16>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP16>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_FP16>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_BF16>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_BF16>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_BF16>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_BF16>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_FP8>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP8>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT8>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_INT8>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT8>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_INT8>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT4>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_INT4>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT4>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_INT4>(int, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT2>(int, bool, bool, bool);
+extern template KernelFn fast_kernel_a64_lg<TBE_TY_INT2>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT2>(int, bool, bool);
 extern template KernelFn nobag_kernel_lg<TBE_TY_INT2>(int, bool);
 
@@ -220,7 +227,18 @@ KernelFn nobag_kernel_group(const TbePlanGroup& g, bool index64) {
 }
 
 KernelFn pooled_kernel_for(const TbePlanGroup& g, bool index64, bool weighted, bool wide, bool wide_words) {
-  if (wide || !g.offset32) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
+  if (wide || g.weight_ty < 0) return weighted ? pooled_wide_kernel<true> : pooled_wide_kernel<false>;
+  if (!g.offset32) {  // past 32-bit byte offsets: 64-bit row addresses
+    switch (g.weight_ty) {
+      case TBE_TY_FP32: return fast_kernel_a64_lg<TBE_TY_FP32>(g.log2_lanes, index64, weighted);
+      case TBE_TY_FP16: return fast_kernel_a64_lg<TBE_TY_FP16>(g.log2_lanes, index64, weighted);
+      case TBE_TY_BF16: return fast_kernel_a64_lg<TBE_TY_BF16>(g.log2_lanes, index64, weighted);
+      case TBE_TY_FP8:  return fast_kernel_a64_lg<TBE_TY_FP8>(g.log2_lanes, index64, weighted);
+      case TBE_TY_INT8: return fast_kernel_a64_lg<TBE_TY_INT8>(g.log2_lanes, index64, weighted);
+      case TBE_TY_INT4: return fast_kernel_a64_lg<TBE_TY_INT4>(g.log2_lanes, index64, weighted);
+      default:          return fast_kernel_a64_lg<TBE_TY_INT2>(g.log2_lanes, index64, weighted);
+    }
+  }
   switch (g.weight_ty) {
     case TBE_TY_FP32: return fast_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64, weighted, wide_words);
     case TBE_TY_FP16: return fast_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64, weighted, wide_words);
@@ -425,7 +443,11 @@ int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_or
     const TbeTableDesc& d = descs[t];
     const bool o32 = d.flags & TBE_TABLE_OFFSET32;
     const bool st = d.flags & TBE_TABLE_STREAM;
-    return o32 ? (d.weight_ty * 8 + d.log2_lanes) * 2 + st : 1000;  // 64-bit tables share one generic kernel
+    const int shape = d.weight_ty * 8 + d.log2_lanes;
+    // tables past 32-bit byte offsets: per shape while rows fit a 32-bit index
+    // (64-bit addresses in the per-bag kernel), else one generic group
+    if (!o32) return d.num_rows < static_cast<int64_t>(kNoRow64) ? 1000 + shape : 100000;
+    return shape * 2 + st;
   };
   std::vector<int32_t> order(T);
   for (int t = 0; t < T; ++t) order[t] = t;
@@ -442,8 +464,9 @@ int tbe_nbit_plan(const TbePlanInput* in, TbeTableDesc* descs, int32_t* table_or
     TbePlanGroup& g = s.groups[s.num_groups++];
     const TbeTableDesc& d0 = descs[order[i]];
     g.offset32 = (d0.flags & TBE_TABLE_OFFSET32) ? 1 : 0;
-    g.weight_ty = g.offset32 ? d0.weight_ty : -1;
-    g.log2_lanes = g.offset32 ? d0.log2_lanes : -1;
+    const bool generic = key(order[i]) == 100000;
+    g.weight_ty = generic ? -1 : d0.weight_ty;
+    g.log2_lanes = generic ? -1 : d0.log2_lanes;
     g.stream = (d0.flags & TBE_TABLE_STREAM) ? 1 : 0;
     g.first = i;
     g.count = j - i;

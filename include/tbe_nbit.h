@@ -99,9 +99,12 @@ typedef struct TbePlanInput {
  * row, same addressing mode.  Their ids are table_order[first .. first+count).
  */
 typedef struct TbePlanGroup {
-  int32_t weight_ty;      /* TbeSparseType                                         */
-  int32_t log2_lanes;     /* as in TbeTableDesc                                    */
-  int32_t offset32;       /* 1: all rows addressed with 32-bit offsets             */
+  int32_t weight_ty;      /* TbeSparseType; -1: the generic 64-bit group (tables of */
+                          /* 2^32 - 1 rows or more, any type and width)            */
+  int32_t log2_lanes;     /* as in TbeTableDesc; -1 for the generic group          */
+  int32_t offset32;       /* 1: all rows addressed with 32-bit offsets; 0: 64-bit  */
+                          /* row addresses (the per-bag kernel's A64 form, or the  */
+                          /* generic kernel when weight_ty is -1)                  */
   int32_t first;          /* position in table_order                               */
   int32_t count;          /* tables in the group                                   */
   int32_t col_tiles;      /* max col_tiles over the group's tables                 */

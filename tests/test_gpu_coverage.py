@@ -1,7 +1,8 @@
 """GPU parity of the paths the random matrices do not reach:
 
-* tables whose rows span more than 4 GiB (64-bit addressing: the generic pooled
-  kernel and the generic nobag kernel), and calls with more than 2^31 indices;
+* tables whose rows span more than 4 GiB (64-bit addressing: the per-bag kernel's
+  64-bit-address form and the generic nobag kernel), and calls with more than 2^31
+  indices (the generic pooled kernel);
 * FP8 rows under exponent-bit / bias pairs other than (4, 7), so both FP8 decodes
   run (fp16 placement for exponent_bits <= 4, shift-and-multiply above);
 * the plan cache under freed and reallocated table metadata;
@@ -79,12 +80,16 @@ def test_big_table_plan_is_64bit(pkg, big_tables):
     descs = plan[0]
     assert not (descs[0].flags & pkg.capi.TBE_TABLE_OFFSET32)
     assert descs[1].flags & pkg.capi.TBE_TABLE_OFFSET32
+    s = plan[2]
+    groups = {(g.weight_ty, g.offset32) for g in s.groups[:s.num_groups]}
+    assert groups == {(INT4, 0), (INT8, 1)}  # the big table keeps its own (A64) group
 
 
 @pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
 @pytest.mark.parametrize("pm,weighted,out_ty", [(0, False, FP16), (1, True, FP32), (0, True, BF16)])
 def test_big_table_pooled(pkg, oracle, gpu, big_tables, idx_dtype, pm, weighted, out_ty):
-    """pooled_wide_kernel on a 4.8 GB table (its last rows, two indices past the end)."""
+    """The per-bag kernel with 64-bit row addresses on a 4.8 GB table (its last rows,
+    two indices past the end, which read the zero row)."""
     m = big_tables
     m.pooling_mode = pkg.PoolingMode(pm)
     m.output_dtype = out_ty

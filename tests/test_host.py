@@ -113,6 +113,20 @@ def test_plan_groups_tables_by_kernel_shape(pkg):
     assert sorted(order.tolist()) == list(range(6))
 
 
+def test_plan_groups_64bit_tables_by_shape(pkg):
+    """Tables past 32-bit byte offsets keep per-shape groups (the per-bag kernel with
+    64-bit addresses) while their rows fit a 32-bit index; only tables of 2^32 - 1
+    rows or more share the generic group (weight_ty -1)."""
+    big = 0xFFFE0000 + 80 * 16
+    woffs = [0, big, 2 * big, 2 * big + 2 ** 34]
+    tys, Ds = [INT4, INT4, INT8, FP32], [128, 128, 128, 1]
+    dofs = np.concatenate([[0], np.cumsum(Ds)])
+    descs, order, s = pkg.capi.plan(woffs, tys, dofs, woffs[3] + 2 ** 32 * 4, row_alignment=4)
+    groups = sorted((g.weight_ty, g.offset32, sorted(order[g.first:g.first + g.count].tolist()))
+                    for g in s.groups[:s.num_groups])
+    assert groups == [(-1, 0, [3]), (INT8, 0, [2]), (INT4, 0, [0, 1])]
+
+
 def test_plan_offset32_covers_tables_below_4gib(pkg):
     """32-bit table addressing (and with it the per-bag and row-stream kernels) holds
     up to 0xFFFE0000 bytes of rows; beyond that the 64-bit kernel takes the table."""
