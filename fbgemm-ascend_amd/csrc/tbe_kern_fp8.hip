@@ -6,5 +6,5 @@ namespace tbe {
 template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool, bool);
 template KernelFn fast_kernel_a64_lg<TBE_TY_FP8>(int, bool, bool);
 template KernelFn stream_kernel_lg<TBE_TY_FP8>(int, bool, bool);
-template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool);
+template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool, bool);
 }  // namespace tbe

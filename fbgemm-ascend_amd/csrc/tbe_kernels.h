@@ -1395,7 +1395,7 @@ __device__ __forceinline__ void decode_word(uint32_t d, float (&v)[Traits<WT>::k
   }
 }
 
-template <int WT, int LG, typename IndexT>
+template <int WT, int LG, typename IndexT, bool A64>
 __device__ __forceinline__ void nobag_segment(const KParams& p, const TbeTableDesc& td, int64_t a, int n) {
   constexpr int E = Traits<WT>::kEpd;
   constexpr bool HDR = Traits<WT>::kHdr;
@@ -1410,8 +1410,11 @@ __device__ __forceinline__ void nobag_segment(const KParams& p, const TbeTableDe
       const_cast<uint8_t*>(p.weights + td.weights_offset), 0, static_cast<int>(rows * stride), kRsrcWord3);
   const uint64_t raw = load_index_chunk<IndexT>(p, a, n);
   const int64_t iv = sizeof(IndexT) == 8 ? static_cast<int64_t>(raw) : static_cast<int64_t>(static_cast<int32_t>(raw));
-  const uint32_t off = (lane < n && iv >= 0 && iv < static_cast<int64_t>(rows)) ? static_cast<uint32_t>(iv) * stride
-                                                                                 : kNoRow;
+  // A64: the row index (kNoRow64 for none); else the row's byte offset (kNoRow)
+  const bool has_row = lane < n && iv >= 0 && iv < static_cast<int64_t>(td.num_rows);
+  const uint32_t off = A64 ? (has_row ? static_cast<uint32_t>(iv) : kNoRow64)
+                           : (has_row ? static_cast<uint32_t>(iv) * stride : kNoRow);
+  const uint8_t* tbase = p.weights + td.weights_offset;
   const bool vec = (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0 && p.out_stride % E == 0;
   for (int ct = 0; ct < td.col_tiles; ++ct) {
     const int dw = ct * kWave + (lane & ((1 << LG) - 1));
@@ -1425,8 +1428,15 @@ __device__ __forceinline__ void nobag_segment(const KParams& p, const TbeTableDe
       for (int u = 0; u < UB; ++u) {
         const uint32_t o = static_cast<uint32_t>(
             __builtin_amdgcn_ds_bpermute(((u0 + u) * R + slot) * 4, static_cast<int>(off)));
-        d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o + col), 0, 0));
-        h[u] = HDR ? static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o), 0, 0)) : 0u;
+        if constexpr (A64) {  // a lane without a row reads the zero row
+          const uint8_t* rp = o != kNoRow64 ? tbase + static_cast<uint64_t>(o) * stride
+                                            : reinterpret_cast<const uint8_t*>(g_zero_row);
+          d[u] = load_word(rp + col);
+          h[u] = HDR ? load_word(rp) : 0u;
+        } else {
+          d[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o + col), 0, 0));
+          h[u] = HDR ? static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o), 0, 0)) : 0u;
+        }
       }
 #pragma unroll
       for (int u = 0; u < UB; ++u) {
@@ -1463,7 +1473,8 @@ __device__ __forceinline__ void nobag_zero_gaps(const KParams& p, int64_t i0, in
   }
 }
 
-template <int WT, int LG, typename IndexT>
+// A64: the group's tables are past 32-bit byte offsets (64-bit row addresses).
+template <int WT, int LG, typename IndexT, bool A64 = false>
 __global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
   const int wv = uniform(threadIdx.x >> 6);
   const int64_t item = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wv;
@@ -1484,8 +1495,9 @@ __global__ __launch_bounds__(kBlock) void nobag_fast_kernel(KParams p) {
     const int64_t a = max(tb, i0), e = min(te, i1);
     if (a >= e) continue;
     const TbeTableDesc td = load_desc(p.tables + t);
-    if (td.weight_ty != WT || td.log2_lanes != LG || !(td.flags & TBE_TABLE_OFFSET32)) continue;
-    nobag_segment<WT, LG, IndexT>(p, td, a, static_cast<int>(e - a));
+    if (td.weight_ty != WT || td.log2_lanes != LG || ((td.flags & TBE_TABLE_OFFSET32) != 0) == A64) continue;
+    if (A64 && td.num_rows >= static_cast<int64_t>(kNoRow64)) continue;  // the generic kernel's
+    nobag_segment<WT, LG, IndexT, A64>(p, td, a, static_cast<int>(e - a));
   }
 }
 
@@ -1628,13 +1640,17 @@ KernelFn stream_kernel_for(bool index64, bool weighted) {
 }
 
 template <int WT>
-KernelFn nobag_kernel_lg(int lg, bool index64) {
+KernelFn nobag_kernel_lg(int lg, bool index64, bool a64) {
   switch (lg) {
-#define TBE_NOBAG_CASE(L) \
-    case L: return index64 ? nobag_fast_kernel<WT, L, int64_t> : nobag_fast_kernel<WT, L, int32_t>;
+#define TBE_NOBAG_CASE(L)                                                                \
+    case L:                                                                              \
+      if (a64) return index64 ? nobag_fast_kernel<WT, L, int64_t, true> : nobag_fast_kernel<WT, L, int32_t, true>; \
+      return index64 ? nobag_fast_kernel<WT, L, int64_t> : nobag_fast_kernel<WT, L, int32_t>;
     TBE_NOBAG_CASE(0) TBE_NOBAG_CASE(1) TBE_NOBAG_CASE(2) TBE_NOBAG_CASE(3) TBE_NOBAG_CASE(4) TBE_NOBAG_CASE(5)
 #undef TBE_NOBAG_CASE
-    default: return index64 ? nobag_fast_kernel<WT, 6, int64_t> : nobag_fast_kernel<WT, 6, int32_t>;
+    default:
+      if (a64) return index64 ? nobag_fast_kernel<WT, 6, int64_t, true> : nobag_fast_kernel<WT, 6, int32_t, true>;
+      return index64 ? nobag_fast_kernel<WT, 6, int64_t> : nobag_fast_kernel<WT, 6, int32_t>;
   }
 }
 

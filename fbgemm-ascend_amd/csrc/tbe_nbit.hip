@@ -19,31 +19,31 @@ namespace tbe {
 extern template KernelFn fast_kernel_lg<TBE_TY_FP32>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_FP32>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP32>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_FP32>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_FP32>(int, bool, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_FP16>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_FP16>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP16>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_FP16>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_FP16>(int, bool, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_BF16>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_BF16>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_BF16>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_BF16>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_BF16>(int, bool, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_FP8>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_FP8>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_FP8>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_FP8>(int, bool, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT8>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_INT8>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT8>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_INT8>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_INT8>(int, bool, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT4>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_INT4>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT4>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_INT4>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_INT4>(int, bool, bool);
 extern template KernelFn fast_kernel_lg<TBE_TY_INT2>(int, bool, bool, bool);
 extern template KernelFn fast_kernel_a64_lg<TBE_TY_INT2>(int, bool, bool);
 extern template KernelFn stream_kernel_lg<TBE_TY_INT2>(int, bool, bool);
-extern template KernelFn nobag_kernel_lg<TBE_TY_INT2>(int, bool);
+extern template KernelFn nobag_kernel_lg<TBE_TY_INT2>(int, bool, bool);
 
 // ---------------------------------------------------------------- nobag (pooling_mode NONE)
 
@@ -109,7 +109,8 @@ __global__ __launch_bounds__(kBlock) void nobag_kernel(KParams p) {
     const int64_t a = max(tb, i0), e = min(te, i1);
     if (a >= e) continue;
     const TbeTableDesc td = load_desc(p.tables + t);
-    if (td.flags & TBE_TABLE_OFFSET32) continue;  // done by the group's specialised kernel
+    // done by the group's specialised kernel (32-bit offsets or 64-bit row addresses)
+    if ((td.flags & TBE_TABLE_OFFSET32) || td.num_rows < static_cast<int64_t>(kNoRow64)) continue;
     switch (td.weight_ty) {
       case TBE_TY_INT4: nobag_rows<TBE_TY_INT4>(p, td, a, e); break;
       case TBE_TY_INT8: nobag_rows<TBE_TY_INT8>(p, td, a, e); break;
@@ -216,13 +217,13 @@ int stream_bags_per_wave(int64_t bags, int64_t resident_waves) {
 // Specialised nobag kernel of a 32-bit group.
 KernelFn nobag_kernel_group(const TbePlanGroup& g, bool index64) {
   switch (g.weight_ty) {
-    case TBE_TY_FP32: return nobag_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64);
-    case TBE_TY_FP16: return nobag_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64);
-    case TBE_TY_BF16: return nobag_kernel_lg<TBE_TY_BF16>(g.log2_lanes, index64);
-    case TBE_TY_FP8:  return nobag_kernel_lg<TBE_TY_FP8>(g.log2_lanes, index64);
-    case TBE_TY_INT8: return nobag_kernel_lg<TBE_TY_INT8>(g.log2_lanes, index64);
-    case TBE_TY_INT4: return nobag_kernel_lg<TBE_TY_INT4>(g.log2_lanes, index64);
-    default:          return nobag_kernel_lg<TBE_TY_INT2>(g.log2_lanes, index64);
+    case TBE_TY_FP32: return nobag_kernel_lg<TBE_TY_FP32>(g.log2_lanes, index64, !g.offset32);
+    case TBE_TY_FP16: return nobag_kernel_lg<TBE_TY_FP16>(g.log2_lanes, index64, !g.offset32);
+    case TBE_TY_BF16: return nobag_kernel_lg<TBE_TY_BF16>(g.log2_lanes, index64, !g.offset32);
+    case TBE_TY_FP8:  return nobag_kernel_lg<TBE_TY_FP8>(g.log2_lanes, index64, !g.offset32);
+    case TBE_TY_INT8: return nobag_kernel_lg<TBE_TY_INT8>(g.log2_lanes, index64, !g.offset32);
+    case TBE_TY_INT4: return nobag_kernel_lg<TBE_TY_INT4>(g.log2_lanes, index64, !g.offset32);
+    default:          return nobag_kernel_lg<TBE_TY_INT2>(g.log2_lanes, index64, !g.offset32);
   }
 }
 
@@ -530,15 +531,15 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     p.order = nullptr;
     const TbePlanSummary& plan = *a->plan;
     if (plan.num_groups < 1 || plan.num_groups > TBE_MAX_GROUPS) return fail(TBE_ERR_INVALID_ARG, "bad plan");
-    // one launch per table group: 32-bit groups take their specialised kernel,
-    // which skips other tables' segments; tables beyond 32-bit addressing take
-    // the generic kernel
+    // one launch per table group: each (type, lanes per row) group takes its
+    // specialised kernel (32-bit offsets or 64-bit row addresses), which skips other
+    // tables' segments; tables of 2^32 - 1 rows or more take the generic kernel
     // the first launch also zeroes the rows of positions outside every segment
     bool generic = false;
     p.zero_gaps = 1;
     for (int gi = 0; gi < plan.num_groups; ++gi) {
       const TbePlanGroup& g = plan.groups[gi];
-      if (!g.offset32) {
+      if (g.weight_ty < 0) {
         generic = true;
         continue;
       }

@@ -1,8 +1,8 @@
 """GPU parity of the paths the random matrices do not reach:
 
-* tables whose rows span more than 4 GiB (64-bit addressing: the per-bag kernel's
-  64-bit-address form and the generic nobag kernel), and calls with more than 2^31
-  indices (the generic pooled kernel);
+* tables whose rows span more than 4 GiB (the 64-bit-address forms of the per-bag
+  and nobag kernels), a table of more than 2^32 rows and calls with more than 2^31
+  indices (the generic kernels);
 * FP8 rows under exponent-bit / bias pairs other than (4, 7), so both FP8 decodes
   run (fp16 placement for exponent_bits <= 4, shift-and-multiply above);
 * the plan cache under freed and reallocated table metadata;
@@ -100,12 +100,54 @@ def test_big_table_pooled(pkg, oracle, gpu, big_tables, idx_dtype, pm, weighted,
 
 @pytest.mark.parametrize("out_ty", [FP16, FP32])
 def test_big_table_nobag(pkg, oracle, gpu, big_tables, out_ty):
-    """The generic nobag kernel (64-bit table) next to the specialised one (small table)."""
+    """The nobag kernel with 64-bit row addresses (big table) next to the 32-bit one
+    (small table)."""
     m = big_tables
     m.pooling_mode = pkg.PoolingMode(2)
     m.output_dtype = out_ty
     idx, off, _ = _big_inputs(gpu, torch.int32)
     _check_module(oracle, m, idx, off, None, f"4.8 GB table nobag out={out_ty}")
+
+
+@pytest.mark.parametrize("pm,weighted", [(0, False), (1, True), (2, False)])
+def test_table_past_2pow32_rows(pkg, oracle, gpu, pm, weighted):
+    """A table of 2^32 + 8 rows (FP32 D=1 at row_alignment 4: 16 GiB), past 32-bit
+    row indices: the generic pooled and nobag kernels, next to a small table that
+    keeps its specialised kernel; int64 indices at both ends of the big table and
+    past it."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    if _free_gib() < 48:
+        pytest.skip("needs ~40 GiB of free HBM")
+    E = 2 ** 32 + 8
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(E, 1, SparseType.FP32), (1000, 1, SparseType.FP32)], device=gpu,
+                                                pooling_mode=pm, output_dtype=FP32, indices_dtype=torch.int64,
+                                                row_alignment=4)
+    try:
+        w = m.weights_dev
+        g = torch.Generator(device=gpu)
+        g.manual_seed(32 + pm)
+        rows_f = w.view(torch.float32)  # one float per row
+        for lo in range(0, rows_f.numel(), 1 << 30):  # U(-1, 1) in slices
+            n = min(1 << 30, rows_f.numel() - lo)
+            rows_f[lo:lo + n] = torch.rand(n, device=gpu, generator=g) * 2 - 1
+        plan = pkg.capi.plan(m.weights_offsets.cpu().numpy(), m.weights_tys.cpu().numpy(),
+                             m.D_offsets.cpu().numpy(), w.numel(), row_alignment=4)
+        s = plan[2]
+        assert sorted(gr.weight_ty for gr in s.groups[:s.num_groups]) == [-1, FP32]
+        B = 64
+        lens = torch.randint(0, 30, (2 * B,), device=gpu, generator=g)
+        off = torch.zeros(2 * B + 1, dtype=torch.int64, device=gpu)
+        torch.cumsum(lens, 0, out=off[1:])
+        n0, N = int(off[B]), int(off[-1])
+        big = torch.randint(E - 3000, E + 2, (n0,), device=gpu, generator=g)  # its last rows, 2 past the end
+        big[::4] = torch.randint(0, 3000, (big[::4].numel(),), device=gpu, generator=g)
+        big[1::4] = torch.randint(0, E, (big[1::4].numel(),), device=gpu, generator=g)
+        idx = torch.cat([big, torch.randint(0, 1000, (N - n0,), device=gpu, generator=g)])
+        psw = torch.rand(N, device=gpu, generator=g) if weighted else None
+        _check_module(oracle, m, idx, off, psw, f"2^32+8 rows pm={pm} w={weighted}")
+    finally:
+        del m
+        torch.cuda.empty_cache()
 
 
 def test_more_than_2pow31_indices(pkg, gpu):
