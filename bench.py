@@ -56,9 +56,12 @@ def _parse():
                     help="HBM traffic per launch measured with rocprofv3 --pmc (JSON); default: "
                          "profiles/tbe_cfg<config>_traffic.json when it exists")
     ap.add_argument("--op", default="tbe",
-                    choices=["tbe", "tbe_nobag", "permute_pooled_embs", "block_bucketize_sparse_features"],
+                    choices=["tbe", "tbe_nobag", "tbe_large_tables", "permute_pooled_embs",
+                             "block_bucketize_sparse_features"],
                     help="tbe: the headline TBE forward; tbe_nobag: the same op with pooling_mode NONE on "
-                         "config 2's tables and indices; permute_pooled_embs: the pooled-output "
+                         "config 2's tables and indices; tbe_large_tables: config 2's bags on 4 tables "
+                         "of 60 M INT4 rows (4.47 GiB each, past 32-bit byte offsets) beside the same "
+                         "lookups on 50 M-row tables; permute_pooled_embs: the pooled-output "
                          "permutation on config 4's output shape; block_bucketize_sparse_features: the "
                          "reference's stress case (16 features x 8192 samples, 128-512 indices, my_size 16)")
     return ap.parse_args()
@@ -172,6 +175,50 @@ def bench_nobag(args, pkg, dev):
                         "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
            "kernel_ms": mean_ms, "kernel_ms_median": ms[len(ms) // 2], "bytes_per_step": nbytes,
            "gather_calibration": calib, "cpu_baseline": None}
+    print(json.dumps(out), flush=True)
+
+
+def bench_large_tables(args, pkg, dev):
+    """Tables past 32-bit byte offsets (a9/a2 of the scope on a 288 GB GPU): config 2's
+    bag lengths and Zipf(1.05) rows on 4 INT4 D=128 tables of 60 M rows (4.47 GiB each,
+    64-bit row addresses), SUM and NONE, timed beside the same lookups on 4 tables of 50 M
+    rows (3.73 GiB, 32-bit offsets).  Batches rotate as in the headline."""
+    import dataclasses
+    import torch
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen
+    from fbgemm_ascend_amd.workloads import config_spec, make_batch
+
+    base = config_spec(2)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for E in (60_000_000, 50_000_000):
+        spec = dataclasses.replace(base, tables=[(E, 128, base.tables[0][2])] * 4)
+        m = IntNBitTableBatchedEmbeddingBagsCodegen(spec.tables, device=dev, pooling_mode=spec.pooling,
+                                                    output_dtype=spec.out_ty, indices_dtype=spec.index_dtype)
+        m.fill_random_weights(0x7BE0 + 2)
+        bs = [make_batch(spec, 0x7BE0 + 3 + 7919 * i, dev) for i in range(max(1, args.batches))]
+        order = [i % len(bs) for i in range(args.steps)]
+        for pm in (0, 2):
+            m.pooling_mode = pkg.PoolingMode(pm)
+            for i in range(args.warmup):
+                b = bs[i % len(bs)]
+                m(b.indices, b.offsets, b.per_sample_weights)
+            ms, wall = time_calls(stream, order, lambda i: m(bs[i].indices, bs[i].offsets, bs[i].per_sample_weights))
+            res[(E, pm)] = (ms, wall)
+        n = sum(b.indices.numel() for b in bs) / len(bs)
+        del m, bs
+        torch.cuda.empty_cache()
+    ms, wall = res[(60_000_000, 0)]
+    out = {"metric": "TBE lookups/s on tables past 4 GiB, 1 GPU", "value": n / (ms * 1e-3), "unit": "lookups/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int4",
+           "data": "synthetic (seeded, generated on device)",
+           "config": {"workload": "4 x 60M INT4 D128 (4.47 GiB per table), config 2 bags B8192 Poisson30 "
+                                  "Zipf1.05, SUM fp16", "lookups": n},
+           "kernel_ms": ms, "nobag_kernel_ms": res[(60_000_000, 2)][0],
+           "below_4gib": {"tables": "4 x 50M INT4 D128 (3.73 GiB)", "kernel_ms": res[(50_000_000, 0)][0],
+                          "nobag_kernel_ms": res[(50_000_000, 2)][0]},
+           "cpu_baseline": None, "roofline": None}
     print(json.dumps(out), flush=True)
 
 
@@ -549,6 +596,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.op == "tbe_nobag":
         bench_nobag(args, pkg, dev)
+        return
+    if args.op == "tbe_large_tables":
+        bench_large_tables(args, pkg, dev)
         return
     if args.op == "permute_pooled_embs":
         bench_permute(args, pkg, dev)
