@@ -186,8 +186,11 @@ __device__ __forceinline__ int64_t load_offset(const KParams& p, int64_t i) {
                    : static_cast<int64_t>(load_uniform(static_cast<const int32_t*>(p.offsets) + i));
 }
 
+// A word of device memory through a global (not flat) load: flat loads also count
+// as LDS operations, so every ds_bpermute wait would wait for them too.
 __device__ __forceinline__ uint32_t load_word(const uint8_t* p) {
-  return *reinterpret_cast<const uint32_t*>(p);
+  using GlobalWord = const __attribute__((address_space(1))) uint32_t;
+  return *(GlobalWord*)(p);
 }
 
 // ---------------------------------------------------------------- element decode
@@ -827,10 +830,17 @@ __device__ __forceinline__ void reduce_store(const KParams& p, const TbeTableDes
   store_out<E2>(p, b * p.out_stride + td.D_offset + static_cast<int64_t>(dw) * EW + e0, r);
 }
 
+// Zeros that a lane without a row reads in its place under 64-bit addressing (no
+// range check there): a zero header and zero words add nothing.  Covers every
+// column offset a lane of a row reads (255 tiles of 64 words after the header).
+constexpr int kZeroRowWords = 256 * kWave + 4;
+static __device__ __align__(16) const uint32_t g_zero_row[kZeroRowWords] = {};
+
 // What a lane needs to gather rows of one bag's table.
 struct BagCtx {
   __amdgpu_buffer_rsrc_t rs;  // the table's rows; range = rows * stride bytes
   const uint8_t* tbase;       // row 0 (64-bit addressing)
+  const uint8_t* zero;        // the zero row (64-bit addressing)
   TbeTableDesc td;
   uint32_t col;               // byte offset of this lane's payload word in a row
   int dw;                     // payload word of this lane
@@ -850,6 +860,7 @@ __device__ __forceinline__ BagCtx bag_ctx(const KParams& p, const StagedBag& sb)
                                                             static_cast<uint32_t>(c.td.row_stride)),
                                            kRsrcWord3);
   c.tbase = p.weights + c.td.weights_offset;
+  c.zero = reinterpret_cast<const uint8_t*>(g_zero_row);
   return c;
 }
 
@@ -868,11 +879,6 @@ __device__ __forceinline__ uint32_t row_offset(const BagCtx& c, uint64_t idx, in
   }
 }
 
-// Zeros that a lane without a row reads in its place under 64-bit addressing (no
-// range check there): a zero header and zero words add nothing.  Covers every
-// column offset a lane of a row reads (255 tiles of 64 words after the header).
-constexpr int kZeroRowWords = 256 * kWave + 4;
-static __device__ __align__(16) const uint32_t g_zero_row[kZeroRowWords] = {};
 
 // VW consecutive words at byte offset `off` of a buffer.
 template <int VW>
@@ -917,9 +923,12 @@ __device__ __forceinline__ void issue_step(const BagCtx& c, uint32_t my_off, flo
       static_assert(VW == 1, "64-bit addressing: one word per lane");
       // off is a row index; a lane without a row reads the zero row (the address
       // is selected, not the loaded value, so no wait is forced here)
-      const uint8_t* zero = reinterpret_cast<const uint8_t*>(g_zero_row);
-      const uint8_t* rp = off != kNoRow64 ? c.tbase + static_cast<uint64_t>(off) * static_cast<uint32_t>(c.td.row_stride)
-                                          : zero;
+      // selected with a mask rather than a branch
+      const uint64_t hit = reinterpret_cast<uint64_t>(c.tbase) +
+                           static_cast<uint64_t>(off) * static_cast<uint32_t>(c.td.row_stride);
+      const uint64_t zr = reinterpret_cast<uint64_t>(c.zero);
+      const uint64_t keep = 0ull - static_cast<uint64_t>(off != kNoRow64);
+      const uint8_t* rp = reinterpret_cast<const uint8_t*>(zr ^ ((hit ^ zr) & keep));
       r.d[u][0] = load_word(rp + c.col);
       if constexpr (Traits<WT>::kHdr) r.h[u] = load_word(rp);
       else r.h[u] = 0u;
