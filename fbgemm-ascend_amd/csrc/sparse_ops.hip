@@ -66,6 +66,16 @@ struct BBParams {
   int32_t keep;
 };
 
+// An element of device memory read through a global (not flat) load.  The position
+// lists are reached through pointers read from memory, which the compiler would
+// otherwise load with flat instructions; a flat load also counts as an LDS
+// operation, so the LDS waits of the histogram and sort code would wait for it.
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  using G = const __attribute__((address_space(1))) T;
+  return *(G*)(p);
+}
+
 __device__ __forceinline__ int64_t uni(int64_t v) {
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v & 0xFFFFFFFF)));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)));
@@ -161,7 +171,7 @@ __device__ __forceinline__ RowCtx<IT> row_ctx_lane(const BBParams<IT, OT>& p, in
     }
   }
   c.scalar = 1;
-  if (c.pos && blk == 0) c.scalar = static_cast<UIT>(static_cast<UIT>(c.pos[c.pos_len - 1]) / c.gb);
+  if (c.pos && blk == 0) c.scalar = static_cast<UIT>(static_cast<UIT>(ldg(c.pos + (c.pos_len - 1))) / c.gb);
   c.fast = !c.pos && blk > 0 && c.lsize > 0 && (static_cast<uint64_t>(c.gsize) >> 32) == 0 &&
            (static_cast<uint64_t>(c.lsize) >> 32) == 0;
   c.dl = make_fastdiv(c.fast ? static_cast<uint32_t>(c.lsize) : 1u);
@@ -238,14 +248,14 @@ __device__ __forceinline__ bool map_index(const RowCtx<IT>& c, std::make_unsigne
     int64_t first = 0, last = c.pos_len;
     while (first < last) {
       const int64_t mid = first + ((last - first) >> 1);
-      if (static_cast<UIT>(c.pos[mid]) <= adj) first = mid + 1; else last = mid;
+      if (static_cast<UIT>(ldg(c.pos + mid)) <= adj) first = mid + 1; else last = mid;
     }
     const int64_t lb = first - 1;
     const bool in = lb >= 0 && static_cast<uint64_t>(lb) < my;
     bucket = in ? lb : static_cast<int64_t>(static_cast<uint64_t>(u) % my);
     if (keep) nidx = static_cast<IT>(u);
     else if (c.blk == 0) nidx = static_cast<IT>(u / c.gb);
-    else if (in) nidx = static_cast<IT>(static_cast<UIT>(u - static_cast<UIT>(c.pos[lb])));
+    else if (in) nidx = static_cast<IT>(static_cast<UIT>(u - static_cast<UIT>(ldg(c.pos + lb))));
     else nidx = static_cast<IT>(static_cast<uint64_t>(u) / my);
   } else if (c.blk != 0 && u < c.gsize) {
     UIT q, r;
