@@ -47,6 +47,7 @@ def _parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target wall time of the CPU leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache measurement")
     ap.add_argument("--no-replay", action="store_true", help="skip the same-batch replay measurement")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay measurement")
     ap.add_argument("--batches", type=int, default=4,
                     help="distinct batches generated before timing and rotated in the timed loop")
     ap.add_argument("--flags", type=int, default=0, help="TBE_FLAG_* tuning switches (C-ABI path)")
@@ -699,7 +700,7 @@ def main():
         del scrub
 
     calib = gather_calibration(wl, stream, timed_span, order, kernel_ms, alg)
-    graph = None if args.flags else graph_replay(calls, K, stream)
+    graph = None if (args.flags or args.no_graph) else graph_replay(calls, K, stream)
 
     traffic = None
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"tbe_cfg{args.config}_traffic.json")
