@@ -109,6 +109,44 @@ def test_big_table_nobag(pkg, oracle, gpu, big_tables, out_ty):
     _check_module(oracle, m, idx, off, None, f"4.8 GB table nobag out={out_ty}")
 
 
+@pytest.mark.parametrize("ty,D", [(FP32, 64), (FP16, 256), (BF16, 128), (FP8, 128), (INT8, 256), (INT2, 64)])
+def test_every_row_type_past_4gib(pkg, oracle, gpu, ty, D):
+    """One table of each row type just past 32-bit byte offsets (64-bit row addresses;
+    FP16 D=256 spans two column tiles): SUM, weighted MEAN and NONE, int32 indices at
+    the end of the table and past it."""
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    from fbgemm_ascend_amd.sparse_types import row_stride
+    if _free_gib() < 16:
+        pytest.skip("needs ~6 GiB of free HBM")
+    st = row_stride(SparseType(ty), D, 16)
+    E = 0xFFFE0000 // st + 4096
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(E, D, SparseType(ty))], device=gpu)
+    try:
+        m.fill_random_weights(ty + 1)
+        plan = pkg.capi.plan(m.weights_offsets.cpu().numpy(), m.weights_tys.cpu().numpy(),
+                             m.D_offsets.cpu().numpy(), m.weights_dev.numel(), 16, m.fp8_exponent_bits,
+                             m.fp8_exponent_bias)
+        assert not (plan[0][0].flags & pkg.capi.TBE_TABLE_OFFSET32)
+        g = torch.Generator(device=gpu)
+        g.manual_seed(400 + ty)
+        B = 48
+        lens = torch.randint(0, 70, (B,), device=gpu, generator=g)
+        off = torch.zeros(B + 1, dtype=torch.int64, device=gpu)
+        torch.cumsum(lens, 0, out=off[1:])
+        N = int(off[-1])
+        idx = torch.randint(E - 8192, E + 2, (N,), device=gpu, generator=g)  # the rows past 4 GiB, 2 past the end
+        idx[::3] = torch.randint(0, E, (idx[::3].numel(),), device=gpu, generator=g)
+        idx, off = idx.to(torch.int32), off.to(torch.int32)
+        psw = torch.rand(N, device=gpu, generator=g)
+        for pm, w, out_ty in ((0, False, FP16), (1, True, FP32), (2, False, BF16)):
+            m.pooling_mode = pkg.PoolingMode(pm)
+            m.output_dtype = out_ty
+            _check_module(oracle, m, idx, off, psw if w else None, f"type {ty} D={D} past 4 GiB pm={pm}")
+    finally:
+        del m
+        torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("pm,weighted", [(0, False), (1, True), (2, False)])
 def test_table_past_2pow32_rows(pkg, oracle, gpu, pm, weighted):
     """A table of 2^32 + 8 rows (FP32 D=1 at row_alignment 4: 16 GiB), past 32-bit
