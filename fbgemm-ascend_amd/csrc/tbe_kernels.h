@@ -642,12 +642,16 @@ __device__ __forceinline__ WaveItems wave_items(const KParams& p) {
 // ---------------------------------------------------------------- pooled bag, 32-bit tables
 
 // Steps (of R = 64 >> LG rows each) whose loads are issued back to back before
-// any is consumed: 16-32 rows in flight per wave for wide rows, a whole 64-index
+// any is consumed: 8-32 rows in flight per wave for wide rows, a whole 64-index
 // chunk for short rows.  U*R always divides 64, so slot r0 + u*R + slot of a
 // step never passes lane 63 and slots past the bag read lanes holding kNoRow.
+// Rows of 32 or more lanes take 8 per lane rather than 16: the two register sets
+// shrink (INT8 D=128: 127 -> 95 VGPRs, 4 -> 5 waves per SIMD) and config 1 runs
+// 43.1 -> 41.3 us, config 3 0.716 -> 0.698 ms; 4 per lane is slower on config 3,
+// and 4 per lane for 16-lane rows (INT4 D=128) takes config 2 from 122 to 140 us.
 template <int LG, int VW = 1>
 constexpr int unroll_for() {
-  return LG >= 5 ? 16 / VW : (LG == 4 ? 8 : kWave / (kWave >> LG));
+  return LG >= 5 ? 8 / VW : (LG == 4 ? 8 : kWave / (kWave >> LG));
 }
 
 // A bag whose first index chunk has been requested: the kernels issue the index
