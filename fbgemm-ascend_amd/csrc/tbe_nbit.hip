@@ -195,15 +195,16 @@ KernelFn stream_kernel_group(const TbePlanGroup& g, bool index64, bool weighted)
 // row-stream kernel by default.
 constexpr int64_t kStreamMinBags = int64_t(1) << 20;
 
-// Bags per wave of the row-stream kernel for a group of `bags` (table, sample)
-// pairs: enough waves for about `rounds` waves per resident wave slot, so the
-// hardware balances the waves' uneven run times, within [4, 63] bags.
-// TBE_STREAM_BAGS_PER_WAVE / TBE_STREAM_ROUNDS override (tuning).
 // Rows a wave of the row-stream kernel should walk: measured on 200 INT4 tables x
 // 32768 bags of ~40 rows, 32 bags per wave (1280 rows) ran 3.14 ms, 24 or 40 bags
 // 3.16 ms, 63 bags 3.20 ms and 16 bags 3.27 ms.
 constexpr int64_t kStreamRowsPerWave = 1280;
 
+// Bags per wave of the row-stream kernel for a group of `bags` (table, sample)
+// pairs: enough waves for about `rounds` waves per resident wave slot, so the
+// hardware balances the waves' uneven run times, and no more bags than hold about
+// kStreamRowsPerWave rows at the call's mean bag length, within [4, 63] bags.
+// TBE_STREAM_BAGS_PER_WAVE / TBE_STREAM_ROUNDS override (tuning).
 int stream_bags_per_wave(int64_t bags, int64_t resident_waves, double rows_per_bag) {
   static const int fixed = [] {
     const char* e = getenv("TBE_STREAM_BAGS_PER_WAVE");
