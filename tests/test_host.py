@@ -330,13 +330,15 @@ def test_plan_fuzz_accepts_or_rejects_cleanly(pkg):
     c = pkg.capi
     rnd = random.Random(1234)
     word_D = {FP32: 1, FP16: 2, BF16: 2, FP8: 4, INT8: 4, INT4: 8, INT2: 16}
-    accepted = rejected = 0
+    accepted = rejected = a64_groups = generic_groups = 0
     for _ in range(600):
         T = rnd.choice([1, 2, 3, 7, 26, 64])
         tys = [rnd.choice([FP32, FP16, INT8, INT4, INT2, BF16, FP8]) for _ in range(T)]
         Ds = [word_D[ty] * rnd.choice([1, 2, 3, 8, 16, 32, 64, 65, 128, 300]) for ty in tys]
         align = rnd.choice([4, 8, 16, 16, 32, 64])
-        rows = [rnd.choice([1, 2, 10, 1000]) for _ in range(T)]
+        # mostly small tables, some past 4 GiB of rows, some of 2^32 rows or more
+        # (the planner only does arithmetic on the sizes: nothing is allocated)
+        rows = [rnd.choice([1, 2, 10, 1000, 1000, 1000, 60_000_000, 2 ** 32 + 5]) for _ in range(T)]
         woffs, pos = [], 0
         for ty, D, E in zip(tys, Ds, rows):
             woffs.append(pos)
@@ -376,13 +378,27 @@ def test_plan_fuzz_accepts_or_rejects_cleanly(pkg):
         seen = []
         for gi in range(s.num_groups):
             g = s.groups[gi]
-            seen += list(order[g.first:g.first + g.count])
+            members = list(order[g.first:g.first + g.count])
+            seen += members
+            a64_groups += int(g.weight_ty >= 0 and not g.offset32)
+            generic_groups += int(g.weight_ty < 0)
+            # a group is one kernel shape: its tables share type, lanes per row and
+            # addressing form (only the generic group, weight_ty -1, mixes them)
+            for t in members:
+                d = descs[t]
+                assert bool(d.flags & c.TBE_TABLE_OFFSET32) == bool(g.offset32)
+                if g.weight_ty >= 0:
+                    assert (d.weight_ty, d.log2_lanes) == (g.weight_ty, g.log2_lanes)
+                    assert bool(d.flags & c.TBE_TABLE_STREAM) == bool(g.stream)
+                else:
+                    assert d.num_rows >= 2 ** 32 - 1 and not g.offset32
         assert sorted(seen) == list(range(T))
         for t in range(T):
             d = descs[t]
             assert d.row_stride > 0 and d.num_rows >= 0
             assert 0 <= d.weights_offset and d.weights_offset + d.num_rows * d.row_stride <= nbytes
     assert accepted > 100 and rejected > 100, (accepted, rejected)
+    assert a64_groups > 20 and generic_groups > 20, (a64_groups, generic_groups)
 
 
 def _stride(ty, D, align):
