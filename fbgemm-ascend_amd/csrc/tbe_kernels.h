@@ -1137,7 +1137,7 @@ constexpr int stream_vw() {
 // work (config 3's INT4 D=256 tables: 148 -> 105 us).  Measured and kept at one
 // word elsewhere: 16-word rows (INT4/INT8/FP16, 3-10 % slower), INT8 and FP16
 // rows of 17-32 words (no gain or up to 6 % slower), 33-64-word rows (15-40 %
-// slower at 2 words: the register ring halves occupancy).
+// slower at 2 words with 16 rows per lane in flight, 3-5 % with 8).
 template <int WT, int LG>
 constexpr int fast_vw() {
   return (LG == 5 && WT == TBE_TY_INT4) ? 2 : 1;
