@@ -1,5 +1,6 @@
-"""The operators under HIP graph capture (torch.cuda.CUDAGraph), and the TBE forward
-called concurrently from several caller streams and host threads.
+"""The operators under HIP graph capture (torch.cuda.CUDAGraph): the TBE forward,
+permute_pooled_embs and block_bucketize_sparse_features; and the TBE forward called
+concurrently from several caller streams and host threads.
 
 A serving loop captures the lookup once and replays it; the TBE forward forks its
 table groups onto library streams and joins them back with events, which must come
@@ -166,3 +167,47 @@ def test_concurrent_caller_streams_and_threads(pkg, gpu):
     for t in th:
         t.join(timeout=120)
     assert not errors, errors
+
+
+@pytest.mark.parametrize("sequence,weighted", [(False, False), (True, True)])
+def test_block_bucketize_graph_replays(pkg, gpu, sequence, weighted):
+    """block_bucketize_sparse_features captured once (its offsets scan, count, scan and
+    scatter kernels) and replayed with new indices and weights of the same lengths."""
+    import numpy as np
+    from _bucketize_cases import CASES, gen_case
+    case = next(c for c in CASES if c.name == "i64_pow2_basic")
+    lengths, indices, block_sizes, w = gen_case(case, 7, weights=weighted)[:4]
+    L = torch.as_tensor(lengths, device=gpu)
+    I = torch.as_tensor(indices, device=gpu)
+    bs = torch.as_tensor(block_sizes, device=gpu)
+    W = torch.as_tensor(w, device=gpu) if weighted else None
+    op = torch.ops.fbgemm.block_bucketize_sparse_features
+
+    def run():
+        return op(L, I, False, sequence, bs, case.my_size, W)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs_g = run()
+    rng = np.random.default_rng(99)
+    for rep in range(3):
+        limit = int(block_sizes.max()) * case.my_size
+        I.copy_(torch.as_tensor(rng.integers(0, limit, indices.size).astype(indices.dtype), device=gpu))
+        if W is not None:
+            W.copy_(torch.rand(W.shape, device=gpu))
+        want = run()  # eager
+        junk = torch.randn(1 << 20, device=gpu).sum()  # other eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for k, (a, b) in enumerate(zip(outs_g, want)):
+            assert (a is None) == (b is None), (rep, k)
+            if a is not None:
+                assert torch.equal(a, b), f"replay {rep}, output {k}"
+        del junk
