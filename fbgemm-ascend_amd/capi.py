@@ -310,6 +310,9 @@ def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, b
     rc = fn(ctypes.byref(a), ctypes.c_void_p(stream))
     if rc != TBE_OK:
         raise TbeError(rc, last_error())
-    torch.cuda.synchronize(dev)  # the temporaries above must outlive the launches
+    # the temporaries above must outlive the launches; under graph capture they stay
+    # in the graph's memory pool, reused only by work captured after these launches
+    if not (indices.is_cuda and torch.cuda.is_current_stream_capturing()):
+        torch.cuda.synchronize(dev)
     del keep, ws, pos_ptrs, pos_lens
     return (new_lengths, new_indices, new_w, new_pos, unb), new_offsets
