@@ -754,6 +754,38 @@ __global__ __launch_bounds__(kBBBlock) void scan_tiles(const T* __restrict__ in,
   if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = T(0);
 }
 
+// Up to this many tiles, each tile's work-group sums the tile sums before it itself
+// (at most 2048 values, from L2) instead of a separate one-work-group pass over them:
+// one launch fewer (the stress case's call: 0.333 -> 0.331 ms).  Above it the sums are
+// scanned by scan_sums_exclusive (the per-tile reads would grow with tiles^2).
+constexpr int64_t kScanBaseMaxTiles = 2048;
+
+template <typename T>
+__global__ __launch_bounds__(kBBBlock) void scan_tiles_based(const T* __restrict__ in, int64_t n,
+                                                             const T* __restrict__ sums, T* __restrict__ out) {
+  __shared__ T lds[kBBBlock / kWaveBB];
+  T part = 0;
+  for (int64_t t = threadIdx.x; t < static_cast<int64_t>(blockIdx.x); t += kBBBlock) part += sums[t];
+  T base;
+  (void)block_exclusive_scan(part, lds, base);  // base = sum of every earlier tile
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x * static_cast<int64_t>(kScanItems);
+  T v[kScanItems];
+  T s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    v[k] = first + k < n ? in[first + k] : T(0);
+    s += v[k];
+  }
+  T total;
+  T run = base + block_exclusive_scan(s, lds, total);
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    run += v[k];
+    if (first + k < n) out[first + k + 1] = run;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = T(0);
+}
+
 int64_t scan_tiles_of(int64_t n) { return (n + kScanTile - 1) / kScanTile; }
 
 int64_t ws_layout(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
@@ -850,10 +882,16 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_of
     hipLaunchKernelGGL((bb_count<IT, OT, false>), dim3(static_cast<uint32_t>(row_blocks)), dim3(kBBBlock), 0, s, p);
   hipLaunchKernelGGL(scan_tile_sums<OT>, dim3(static_cast<uint32_t>(tiles)), dim3(kBBBlock), 0, s,
                      const_cast<const OT*>(p.new_lengths), nseg, sums);
-  hipLaunchKernelGGL(scan_sums_exclusive<OT>, dim3(1), dim3(kBBBlock), 0, s, sums, tiles);
-  hipLaunchKernelGGL(scan_tiles<OT>, dim3(static_cast<uint32_t>(tiles)), dim3(kBBBlock), 0, s,
-                     const_cast<const OT*>(p.new_lengths), nseg, const_cast<const OT*>(sums),
-                     static_cast<OT*>(a->new_offsets));
+  if (tiles <= kScanBaseMaxTiles) {
+    hipLaunchKernelGGL(scan_tiles_based<OT>, dim3(static_cast<uint32_t>(tiles)), dim3(kBBBlock), 0, s,
+                       const_cast<const OT*>(p.new_lengths), nseg, const_cast<const OT*>(sums),
+                       static_cast<OT*>(a->new_offsets));
+  } else {
+    hipLaunchKernelGGL(scan_sums_exclusive<OT>, dim3(1), dim3(kBBBlock), 0, s, sums, tiles);
+    hipLaunchKernelGGL(scan_tiles<OT>, dim3(static_cast<uint32_t>(tiles)), dim3(kBBBlock), 0, s,
+                       const_cast<const OT*>(p.new_lengths), nseg, const_cast<const OT*>(sums),
+                       static_cast<OT*>(a->new_offsets));
+  }
   if (p.N > 0) {
     const dim3 g(static_cast<uint32_t>(row_blocks));
     if (!reg) hipLaunchKernelGGL((bb_scatter<IT, OT, 0>), g, dim3(kBBBlock), 0, s, p);
