@@ -642,6 +642,8 @@ int tbe_nbit_forward(const TbeNbitArgs* a, void* hip_stream) {
     } else {
       const int64_t items = static_cast<int64_t>(g.count) * a->B * g.col_tiles;
       p.num_items = static_cast<int32_t>(items);
+      // progress-ordered wave priority only when this group's kernel runs alone
+      p.xcd = (p.xcd & 1) | (plan.num_groups == 1 ? 2 : 0);
       // two words per lane when every table of the group has an even word count
       const bool wide_words = g.stream && !(a->flags & TBE_FLAG_NARROW_WORDS);
       err = launch(pooled_kernel_for(g, p.index64 != 0, weighted, wide, wide_words), p,
