@@ -266,10 +266,12 @@ def permute_pooled_embs(pooled_embs, offset_dim_list, permute_list, inv_offset_d
 
 def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, block_sizes, my_size,
                                     weights=None, batch_size_per_feature=None, block_bucketize_pos=None,
-                                    keep_orig_idx=False, total_num_blocks=None, noalloc=False):
+                                    keep_orig_idx=False, total_num_blocks=None, noalloc=False, sync=True):
     """tbe_block_bucketize_sparse_features on torch device tensors; returns the op's
     five outputs (None where not requested) plus new_offsets.  noalloc=True calls
-    tbe_block_bucketize_sparse_features_noalloc instead (no workspace passed)."""
+    tbe_block_bucketize_sparse_features_noalloc instead (no workspace passed).
+    sync=False returns without waiting for the launches (the temporaries the call
+    reads are kept alive by new_offsets until it is freed)."""
     import torch
 
     dev = indices.device
@@ -312,7 +314,9 @@ def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, b
         raise TbeError(rc, last_error())
     # the temporaries above must outlive the launches; under graph capture they stay
     # in the graph's memory pool, reused only by work captured after these launches
-    if not (indices.is_cuda and torch.cuda.is_current_stream_capturing()):
+    if not sync:
+        new_offsets._tbe_keep = (keep, ws, pos_ptrs, pos_lens)
+    elif not (indices.is_cuda and torch.cuda.is_current_stream_capturing()):
         torch.cuda.synchronize(dev)
     del keep, ws, pos_ptrs, pos_lens
     return (new_lengths, new_indices, new_w, new_pos, unb), new_offsets

@@ -804,28 +804,46 @@ constexpr int64_t kNoAllocScratchBytes = TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYT
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of this GPU's scratch array (looked up once per device, with the
-// device current).  Returns nullptr and sets the error on failure.
-void* scratch_for_current_device() {
+// Per-GPU state of the entry point that allocates nothing, set up on its first call
+// on that GPU (with the GPU current): the scratch array's device address, and an
+// event recorded after every eager call, which the next eager call on that GPU (any
+// stream, any thread) waits for, so calls that would overlap run one after another
+// on the shared scratch instead of racing on it.
+struct NoAllocDevice {
+  void* scratch = nullptr;
+  hipEvent_t done = nullptr;
+  bool recorded = false;
+};
+std::mutex g_noalloc_mu;  // held across a call's set-up, wait, launches and record
+NoAllocDevice g_noalloc[kMaxDevices];
+
+// This GPU's state (g_noalloc_mu held).  Returns nullptr and sets the error on failure.
+NoAllocDevice* noalloc_device() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     fail(TBE_ERR_LAUNCH, "no current HIP device");
     return nullptr;
   }
-  std::lock_guard<std::mutex> g(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  NoAllocDevice& d = g_noalloc[dev];
+  if (!d.scratch) {
     void* ptr = nullptr;
     const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (err != hipSuccess || !ptr) {
       fail(TBE_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(err));
       return nullptr;
     }
-    g_scratch_ptr[dev] = ptr;
+    d.scratch = ptr;
   }
-  return g_scratch_ptr[dev];
+  if (!d.done) {
+    const hipError_t err = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+    if (err != hipSuccess) {
+      d.done = nullptr;
+      fail(TBE_ERR_LAUNCH, "hipEventCreateWithFlags failed: %s", hipGetErrorString(err));
+      return nullptr;
+    }
+  }
+  return &d;
 }
 
 // Scratch bytes a call needs: the per-segment write cursors (my_size > 64 only;
@@ -977,7 +995,23 @@ extern "C" int tbe_block_bucketize_sparse_features_noalloc(const TbeBlockBucketi
                 "tbe_block_bucketize_sparse_features with a workspace",
                 static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
   if (check_pointers(a) != TBE_OK) return TBE_ERR_INVALID_ARG;
-  void* ws = scratch_for_current_device();
-  if (!ws) return TBE_ERR_LAUNCH;
-  return dispatch(a, static_cast<hipStream_t>(hip_stream), ws, sums_off);
+  const hipStream_t s = static_cast<hipStream_t>(hip_stream);
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoAllocDevice* d = noalloc_device();
+  if (!d) return TBE_ERR_LAUNCH;
+  // Eager calls wait for the previous call on this GPU.  Under graph capture the
+  // graph orders the captured call; a wait on (or record of) an event from outside
+  // the capture would break the capture, so neither is done there.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess)
+    return fail(TBE_ERR_LAUNCH, "hipStreamIsCapturing failed");
+  const bool eager = cs == hipStreamCaptureStatusNone;
+  if (eager && d->recorded && hipStreamWaitEvent(s, d->done, 0) != hipSuccess)
+    return fail(TBE_ERR_LAUNCH, "hipStreamWaitEvent on the previous call failed");
+  const int rc2 = dispatch(a, s, d->scratch, sums_off);
+  if (eager && rc2 == TBE_OK) {
+    if (hipEventRecord(d->done, s) != hipSuccess) return fail(TBE_ERR_LAUNCH, "hipEventRecord failed");
+    d->recorded = true;
+  }
+  return rc2;
 }

@@ -95,9 +95,16 @@ int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* args, void*
  *   (my_size > 64 ? roundup(4 * my_size * lengths_size, 256) : 0)
  *   + offset_size * max(1, ceil(my_size * lengths_size / 1024))
  * bytes of it; larger calls are rejected with TBE_ERR_UNSUPPORTED and a message.
- * Every call on one GPU shares that GPU's array: calls that overlap in time on
- * one GPU (on different streams, or from several threads without ordering) race
- * on it and give wrong results.  Calls queued on one stream are ordered and safe.
+ * Every call on one GPU shares that GPU's array, so calls on one GPU are made
+ * to run one after another: each call (from any stream or host thread) first
+ * makes its stream wait for an event recorded after the previous call on that
+ * GPU, then records it after its own kernels; calls on different streams are
+ * therefore serialised on the GPU rather than overlapped.  The first call on a GPU
+ * looks up the array's address and creates that event.  A call made while its
+ * stream is being captured into a HIP graph neither waits nor records (an event
+ * from outside the capture cannot be waited on inside it): the graph orders the
+ * captured call, and a replay must not run at the same time as another call on
+ * the same GPU.
  */
 #define TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES (32LL << 20)
 int tbe_block_bucketize_sparse_features_noalloc(const TbeBlockBucketizeArgs* args, void* hip_stream);

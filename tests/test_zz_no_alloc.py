@@ -100,3 +100,80 @@ def test_noalloc_under_graph_capture(pkg, gpu):
             assert (a is None) == (b is None), (rep, k)
             if a is not None:
                 assert torch.equal(a, b), f"replay {rep}, output {k}"
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(pkg, gpu):
+    """Calls on two streams, launched back to back with no host synchronisation, share
+    the GPU's scratch (my_size > 64: the write cursors live there); each call waits for
+    the previous one on the GPU, so both equal the workspace entry point's results."""
+    from fbgemm_ascend_amd import capi
+    names = ["new_lengths", "new_indices", "new_weights", "new_pos", "unbucketize_permute"]
+    ins = []
+    for seed in (31, 32):
+        lengths, indices, block_sizes, w = gen_case(WIDE, seed, True)
+        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+        ins.append((d(lengths), d(indices), d(block_sizes), d(w)))
+    want = [capi.block_bucketize_sparse_features(L, I, True, True, bs, WIDE.my_size, weights=w)
+            for L, I, bs, w in ins]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        print(f"[gpu] noalloc on two streams, round {rep}", flush=True)
+        got = []
+        for (L, I, bs, w), st in zip(ins, streams):
+            with torch.cuda.stream(st):
+                got.append(capi.block_bucketize_sparse_features(L, I, True, True, bs, WIDE.my_size, weights=w,
+                                                                noalloc=True, sync=False))
+        torch.cuda.synchronize()
+        for k, ((go, goff), (wo, woff)) in enumerate(zip(got, want)):
+            assert torch.equal(goff, woff), f"round {rep}, call {k}: new_offsets"
+            for n, a, b in zip(names, go, wo):
+                assert torch.equal(a, b), f"round {rep}, call {k}: {n}"
+
+
+_CAPTURE_FIRST = r"""
+import sys
+import numpy as np
+import torch
+sys.path[:0] = [sys.argv[1], sys.argv[1] + "/tests"]
+import __graft_entry__ as graft
+graft.load_package()
+from fbgemm_ascend_amd import capi
+from _bucketize_cases import CASES, gen_case
+case = {c.name: c for c in CASES}["i64_pow2_basic"]
+lengths, indices, block_sizes, _ = gen_case(case, 5)
+L = torch.as_tensor(lengths, device="cuda:0")
+I = torch.as_tensor(indices, device="cuda:0")
+bs = torch.as_tensor(block_sizes, device="cuda:0")
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):  # the process's first call of the entry point
+    outs, off = capi.block_bucketize_sparse_features(L, I, True, True, bs, case.my_size, noalloc=True)
+for rep in range(3):
+    g.replay()
+    torch.cuda.synchronize()
+    want, want_off = capi.block_bucketize_sparse_features(L, I, True, True, bs, case.my_size)
+    assert torch.equal(off, want_off), f"replay {rep}: new_offsets"
+    for a, b in zip(outs, want):
+        assert (a is None) == (b is None)
+        assert a is None or torch.equal(a, b), f"replay {rep}"
+print("capture-first OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture(pkg, gpu, tmp_path):
+    """A process whose first call of the entry point is made under HIP graph capture:
+    the per-GPU set-up (scratch address, ordering event) happens inside the capture,
+    and the replays equal the workspace entry point (fresh process, so no earlier call
+    has done the set-up)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "capture_first.py"
+    script.write_text(_CAPTURE_FIRST)
+    print("[gpu] noalloc first call under capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, str(script), root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "capture-first OK" in r.stdout
