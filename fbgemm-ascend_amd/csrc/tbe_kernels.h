@@ -1543,13 +1543,15 @@ __global__ __launch_bounds__(kBlock) void pooled_fast_kernel(KParams p) {
   // starts at priority 3 and drops one level per quarter of its items, so at any
   // moment the waves that are behind issue first, and the kernel's last waves are
   // the ones that were slowest (config 2 123.6 -> 117.9 us, config 1 42.0 -> 39.9 us).
-  // Next to other groups' kernels on other streams it is left off (the thresholds
-  // are out of reach): there, fresh waves of the next kernel at priority 3 held
-  // back the previous kernel's last waves (config 3 0.70 -> 0.72 ms).
-  const uint32_t off_q = (p.xcd & 2) ? 0u : 0x7FFFFFFFu;
-  const uint32_t q1 = uniform(static_cast<int>((nitems >> 2) | off_q));
-  const uint32_t q2 = uniform(static_cast<int>((nitems >> 1) | off_q));
-  const uint32_t q3 = uniform(static_cast<int>(((nitems >> 2) + (nitems >> 1)) | off_q));
+  // Next to other groups' kernels on other streams it is off: the thresholds are
+  // all zero, so the first check (g = 0) drops the wave to priority 0 before its
+  // first bag (a separate branch around the first s_setprio costs the INT4 kernel
+  // 20 VGPRs and a wave per SIMD); at priority 3 throughout, fresh waves of the
+  // next kernel held back the previous kernel's last waves (config 3 0.70 -> 0.72 ms).
+  const uint32_t on_q = (p.xcd & 2) ? 0xFFFFFFFFu : 0u;
+  const uint32_t q1 = uniform(static_cast<int>((nitems >> 2) & on_q));
+  const uint32_t q2 = uniform(static_cast<int>((nitems >> 1) & on_q));
+  const uint32_t q3 = uniform(static_cast<int>(((nitems >> 2) + (nitems >> 1)) & on_q));
   __builtin_amdgcn_s_setprio(3);
   while (true) {
     if ((g & 3) == 0) {
