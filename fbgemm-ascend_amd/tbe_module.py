@@ -79,6 +79,7 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
         self.device_ = torch.device(device)
         self.pooling_mode = PoolingMode(int(pooling_mode))
         self.output_dtype = int(output_dtype)
+        self._lookup = None  # the op's default overload, resolved at the first forward
         self.indices_dtype = indices_dtype
         self.row_alignment = int(row_alignment)
         for E, D, ty in self.specs:
@@ -205,14 +206,14 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
     # ------------------------------------------------------------------ forward
     def forward(self, indices: torch.Tensor, offsets: torch.Tensor,
                 per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
-        return torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(
-            dev_weights=self.weights_dev, uvm_weights=self.weights_uvm,
-            weights_placements=self.weights_placements, weights_offsets=self.weights_offsets,
-            weights_tys=self.weights_tys, D_offsets=self.D_offsets, total_D=self.total_D,
-            max_int2_D=self.max_int2_D, max_int4_D=self.max_int4_D, max_int8_D=self.max_int8_D,
-            max_float16_D=self.max_float16_D, max_float32_D=self.max_float32_D,
-            indices=indices, offsets=offsets, pooling_mode=int(self.pooling_mode),
-            indice_weights=per_sample_weights, output_dtype=self.output_dtype,
-            lxu_cache_weights=None, lxu_cache_locations=None, row_alignment=self.row_alignment,
-            max_float8_D=self.max_float8_D, fp8_exponent_bits=self.fp8_exponent_bits,
-            fp8_exponent_bias=self.fp8_exponent_bias)
+        # the op's overload resolved once and called with positional arguments in
+        # schema order: keyword parsing and overload lookup cost more host time per
+        # call than the launch itself on small batches
+        op = self._lookup
+        if op is None:
+            op = self._lookup = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function.default
+        return op(self.weights_dev, self.weights_uvm, self.weights_placements, self.weights_offsets,
+                  self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,
+                  self.max_int8_D, self.max_float16_D, self.max_float32_D, indices, offsets,
+                  int(self.pooling_mode), per_sample_weights, self.output_dtype, None, None, self.row_alignment,
+                  self.max_float8_D, self.fp8_exponent_bits, self.fp8_exponent_bias)
