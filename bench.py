@@ -223,24 +223,6 @@ def bench_large_tables(args, pkg, dev):
     print(json.dumps(out), flush=True)
 
 
-def calib_chunks(first, n: int):
-    """Per 64-lookup chunk c of lookups [64 c, 64 c + 64) (tbe_calib_gather's `chunk`
-    records): {table of lookup 64 c, the table after the first boundary inside the chunk,
-    the lane of that boundary (64: none), 1 if a further table starts inside the chunk}.
-    `first` [T + 1] holds every table's first lookup (first[T] = n); empty tables share
-    their first position with the next table."""
-    import torch
-    T = first.numel() - 1
-    starts = torch.arange(0, n, 64, device=first.device, dtype=torch.int64)
-    ta = (torch.searchsorted(first, starts, right=True) - 1).clamp_(0, T - 1)       # table of the first lookup
-    tb = (torch.searchsorted(first, starts + 63, right=True) - 1).clamp_(0, T - 1)  # table of the last one
-    split = torch.where(tb > ta, first[ta + 1] - starts, torch.full_like(starts, 64))
-    tnext = (torch.searchsorted(first, starts + split.clamp(max=63), right=True) - 1).clamp_(0, T - 1)
-    more = (tb > tnext).to(torch.int64)
-    second = torch.where(tb > ta, tnext, (ta + 1).clamp(max=T - 1))
-    return torch.stack([ta, second, split, more], 1).to(torch.int32).contiguous()
-
-
 def time_calls(stream, order, fn):
     """fn(i) for every i of `order` between one pair of HIP events on `stream`; returns
     (GPU ms per call, wall s)."""
@@ -256,63 +238,110 @@ def time_calls(stream, order, fn):
     return a.elapsed_time(b) / len(order), time.perf_counter() - t0
 
 
-def gather_calibration(wl, stream, timed, order, op_ms, alg, out_bytes=None):
-    """The same batches through libtbe_calib.so's tbe_calib_gather: every lookup's unpadded
-    row read (one row per lane, 16-byte loads, index order) and an output-sized buffer
-    written, with no arithmetic and no bag structure.  Its time is the practical floor of
-    the operator's memory work on this workload; `op_over_floor` is the operator's time
-    over it (`timed(order, fn)` returns GPU ms per call and wall seconds; `op_ms` is the
-    operator's ms per call measured the same way).  None when the library is not built,
-    the tables' row sizes differ (config 3), a row stride is not a multiple of 16 or a
-    row is above 512 bytes."""
-    import ctypes
-    import numpy as np
+def row_addresses(wl, i: int):
+    """Byte address of every lookup's row (header first) in batch i, int64 [N] on the
+    device; computed outside any timed region."""
     import torch
-    from fbgemm_ascend_amd.sparse_types import unpadded_row_bytes
+    m, bt = wl.module, wl.batches[i]
+    dev = bt.indices.device
+    T, B = len(m.specs), wl.spec.B
+    per_table = bt.lengths.view(T, B).sum(dim=1)
+    table = torch.repeat_interleave(torch.arange(T, device=dev), per_table)
+    wo = m.weights_offsets.to(dev, torch.int64)
+    stride = torch.as_tensor([int(x) for x in m.row_strides], dtype=torch.int64, device=dev)
+    return (m.weights_dev.data_ptr() + wo[table] + bt.indices.to(torch.int64) * stride[table]).contiguous()
 
-    path = os.path.join(ROOT, "fbgemm-ascend_amd", "libtbe_calib.so")
+
+def gather_calibration(wl, stream, timed, order, op_ms, alg, out_bytes=None):
+    """The same batches through measure/libtbe_floor.so's tbe_gather_floor: every lookup's
+    header word and payload words gathered (the lines the operator fetches) by persistent
+    waves that do nothing else (64-lookup chunks, the next chunk's rows in flight), and
+    about the operator's output bytes written.  Its time is a floor of the operator's
+    memory work on this workload; `op_over_floor` is the operator's time over it
+    (`timed(order, fn)` returns GPU ms per call and wall seconds; `op_ms` is the
+    operator's ms per call measured the same way).  None when the library is not built
+    or the tables are not INT rows of one payload size up to 32 words."""
+    import ctypes
+    import torch
+    from fbgemm_ascend_amd.sparse_types import SparseType, unpadded_row_bytes
+
+    path = os.path.join(ROOT, "measure", "libtbe_floor.so")
     m = wl.module
     sizes = {unpadded_row_bytes(ty, D) for (_, D, ty) in m.specs}
-    if (not os.path.exists(path) or len(sizes) != 1 or max(sizes) > 512
-            or any(int(st) % 16 or E >= 2 ** 32 for st, (E, _, _) in zip(m.row_strides, m.specs))):
+    int_rows = all(ty in (SparseType.INT8, SparseType.INT4, SparseType.INT2) for (_, _, ty) in m.specs)
+    if not os.path.exists(path) or len(sizes) != 1 or not int_rows:
+        return None
+    payload_words = (sizes.pop() - 4) // 4
+    if payload_words > 32:
         return None
     lib = ctypes.CDLL(path)
-    lib.tbe_calib_gather.restype = ctypes.c_int
-    dev = wl.indices.device
-    T = len(m.specs)
-    B = wl.spec.B
-    wo = m.weights_offsets.cpu().tolist()
-    desc = np.array([[wo[t] & 0xFFFFFFFF, wo[t] >> 32, int(m.row_strides[t]) | (unpadded_row_bytes(ty, D) << 16), E]
-                     for t, (E, D, ty) in enumerate(m.specs)], dtype=np.uint32)
-    desc = torch.from_numpy(desc.view(np.int32)).to(dev)
-    row_bytes = sizes.pop()
+    lib.tbe_gather_floor.restype = ctypes.c_int
+    addrs = [row_addresses(wl, i) for i in range(len(wl.batches))]
+    n_max = max(a.numel() for a in addrs)
     out_sz = {0: 4, 1: 2, 5: 2}[m.output_dtype]
-    out_units = (B * m.total_D * out_sz if out_bytes is None else out_bytes) // 8
-    out = torch.empty(max(1, out_units), dtype=torch.int64, device=dev)
-    sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    firsts, chunks = [], []
-    for bt in wl.batches:
-        f = bt.offsets.to(torch.int64)[torch.arange(T + 1, device=dev) * B].contiguous()
-        firsts.append(f)
-        chunks.append(calib_chunks(f, bt.indices.numel()))
+    obytes = wl.spec.B * m.total_D * out_sz if out_bytes is None else out_bytes
+    out_words = max(1, round(obytes / max(1, wl.num_indices) / 4))
+    out = torch.empty(max(1, n_max * out_words), dtype=torch.int32, device=addrs[0].device)
+    fallback = m.weights_dev.data_ptr()
     P = ctypes.c_void_p
 
     def run(i):
-        bt = wl.batches[i]
-        rc = lib.tbe_calib_gather(P(m.weights_dev.data_ptr()), P(bt.indices.data_ptr()),
-                                  ctypes.c_int(bt.indices.element_size()), P(firsts[i].data_ptr()),
-                                  P(desc.data_ptr()), P(chunks[i].data_ptr()), ctypes.c_int32(row_bytes),
-                                  ctypes.c_int64(bt.indices.numel()), P(out.data_ptr()), ctypes.c_int64(out_units),
-                                  P(sink.data_ptr()), P(stream.cuda_stream))
+        a = addrs[i]
+        rc = lib.tbe_gather_floor(P(a.data_ptr()), ctypes.c_int64(a.numel()), ctypes.c_uint64(fallback),
+                                  ctypes.c_int32(payload_words), P(out.data_ptr()), ctypes.c_int32(out_words),
+                                  P(stream.cuda_stream))
         if rc != 0:
-            raise RuntimeError(f"tbe_calib_gather failed ({rc})")
+            raise RuntimeError(f"tbe_gather_floor failed ({rc})")
 
     for i in range(len(wl.batches)):
         run(i)
     floor_ms, _ = timed(order, fn=run)
     total_alg = sum(alg[i] for i in order)
     return {"kernel_ms": floor_ms, "frac": total_alg / (floor_ms * len(order) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-            "op_over_floor": op_ms / floor_ms}
+            "op_over_floor": op_ms / floor_ms, "out_words_per_lookup": out_words}
+
+
+def cold_cache_times(calls, K: int, alg, stream, n: int):
+    """The op with nothing of its tables in the L2 or the memory-side cache: before each
+    call a 512 MiB scrub (larger than the 32 MB of L2 and the 256 MB memory-side cache)
+    evicts them.  Timed without an event pair around each call: one event pair around n
+    (scrub, call) pairs and one around the n scrubs alone; the call's time is the
+    difference over n.  Two scrubs: `cold_cache` reads the buffer (a max reduction), so
+    the caches hold clean scrub lines; `cold_cache_dirty` writes it (a fill), so the call
+    also pays for writing back the dirty scrub lines it evicts."""
+    import torch
+    scrub = torch.empty(512 * 2 ** 20 // 4, dtype=torch.int32, device=stream.device)
+    scrub.fill_(1)
+
+    def span(fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for i in range(n):
+            fn(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b)
+
+    out = []
+    for kind in ("read", "write"):
+        if kind == "read":
+            def s(i):
+                return torch.amax(scrub)
+        else:
+            def s(i):
+                scrub.fill_(i & 0x7F)
+
+        def pair(i, s=s):
+            s(i)
+            calls[i % K]()
+
+        span(pair)  # warm-up of both kernels
+        ms = (span(pair) - span(s)) / n
+        alg_mean = sum(alg[i % K] for i in range(n)) / n
+        out.append({"kernel_ms": ms, "frac": alg_mean / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, "scrub": kind})
+    del scrub
+    return out[0], out[1]
 
 
 def graph_replay(calls, K: int, stream, per_graph: int = 20, replays: int = 10):
@@ -683,21 +712,9 @@ def main():
     if not args.no_replay:
         replay_kernel_ms, _ = timed_span([0] * args.steps)
 
-    cold_ms = None
+    cold = cold_dirty = None
     if not args.no_cold:
-        scrub = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=dev)
-        cold = []
-        for i in range(min(args.steps, 20)):
-            scrub.fill_(i & 0xFF)  # evict L2 and MALL between calls
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            calls[i % K]()
-            b.record(stream)
-            torch.cuda.synchronize()
-            cold.append((a.elapsed_time(b), i % K))
-        cold_ms = sum(c for c, _ in cold) / len(cold)
-        cold_alg = sum(alg[i] for _, i in cold) / len(cold)
-        del scrub
+        cold, cold_dirty = cold_cache_times(calls, K, alg, stream, min(args.steps, 20))
 
     calib = gather_calibration(wl, stream, timed_span, order, kernel_ms, alg)
     graph = None if (args.flags or args.no_graph) else graph_replay(calls, K, stream)
@@ -743,7 +760,8 @@ def main():
         "bags_per_s": wl.num_bags * args.steps / wall,
         "replay_same_batch": ({"kernel_ms": replay_kernel_ms, "frac": frac(replay_kernel_ms, alg[0])}
                               if replay_kernel_ms is not None else None),
-        "cold_cache": ({"kernel_ms": cold_ms, "frac": frac(cold_ms, cold_alg)} if cold_ms is not None else None),
+        "cold_cache": cold,
+        "cold_cache_dirty": cold_dirty,
         "gather_calibration": calib,
         "graph_replay": graph,
     }

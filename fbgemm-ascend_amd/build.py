@@ -105,19 +105,9 @@ def build_torch_binding():
     _run(cmd)
 
 
-CALIB_LIB = os.path.join(PKG_DIR, "libtbe_calib.so")
-
-
-def build_calib_lib():
-    """libtbe_calib.so: the measurement kernel of bench.py --gather-calibration."""
-    hipcc = os.path.join(ROCM, "bin", "hipcc")
-    _run([hipcc, *HIP_FLAGS, "-shared", os.path.join(CSRC, "calib_gather.hip"), "-o", CALIB_LIB])
-
-
 def build():
     build_hip_lib()
     build_torch_binding()
-    build_calib_lib()
 
 
 def build_sanitized():

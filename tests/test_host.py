@@ -290,33 +290,27 @@ def test_module_fp8_quantize_roundtrip(pkg, oracle, eb, bias):
     assert bool(((torch.from_numpy(out).double() - w.float().double()).abs() <= half_step).all())
 
 
-def test_calibration_chunk_records_find_every_lookups_table():
-    """bench.calib_chunks: with the kernel's rule (lanes below the split take the first
-    table, the rest the second, walking forward only when a further table starts in the
-    chunk) every lookup lands in its table, including empty and 1-lookup tables."""
-    import random
+def test_gather_floor_row_addresses(pkg):
+    """bench.row_addresses (the gather floor's input): every lookup's address is the
+    table base + index * row stride of the lookup's table, including empty bags and
+    tables of different strides."""
     import sys
     sys.path.insert(0, ROOT)
     import bench
-    rnd = random.Random(7)
-    for _ in range(150):
-        T = rnd.randint(1, 30)
-        lens = [rnd.choice([0, 0, 1, 5, 63, 64, 65, 200, 1000]) for _ in range(T)]
-        first = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int64)
-        n = int(first[-1])
-        if n == 0:
-            continue
-        c = bench.calib_chunks(first, n).tolist()
-        f = first.tolist()
-        for i in range(n):
-            truth = int(np.searchsorted(f, i, side="right")) - 1
-            ta, tb, split, more = c[i >> 6]
-            lane = i & 63
-            t = ta if lane < split else tb
-            if more and lane >= split:
-                while f[t + 1] <= i:
-                    t += 1
-            assert t == truth, (i, t, truth, c[i >> 6], f)
+    from fbgemm_ascend_amd.workloads import make_workload
+    wl = make_workload(3, device="cpu", scale_rows=1e-4, batch=6, table_limit=7)
+    m = wl.module
+    for i in range(len(wl.batches)):
+        bt = wl.batches[i]
+        got = bench.row_addresses(wl, i).tolist()
+        off = bt.offsets.tolist()
+        B = wl.spec.B
+        want = []
+        for t in range(len(m.specs)):
+            for j in range(off[t * B], off[(t + 1) * B]):
+                want.append(m.weights_dev.data_ptr() + int(m.weights_offsets[t]) +
+                            int(bt.indices[j]) * int(m.row_strides[t]))
+        assert got == want
 
 
 def test_plan_fuzz_accepts_or_rejects_cleanly(pkg):
