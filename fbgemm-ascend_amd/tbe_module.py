@@ -68,6 +68,11 @@ def _spec_fields(spec) -> Tuple[int, int, SparseType]:
     return int(E), int(D), SparseType(int(ty))
 
 
+# The lookup op's default overload, resolved at the first forward (the op is registered
+# when the package is imported; a module-level cache keeps modules picklable).
+_LOOKUP = None
+
+
 class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
     def __init__(self, embedding_specs: Sequence, device="cuda", pooling_mode=PoolingMode.SUM,
                  output_dtype=SparseType.FP16, indices_dtype=torch.int32, row_alignment: int = 16,
@@ -79,7 +84,6 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
         self.device_ = torch.device(device)
         self.pooling_mode = PoolingMode(int(pooling_mode))
         self.output_dtype = int(output_dtype)
-        self._lookup = None  # the op's default overload, resolved at the first forward
         self.indices_dtype = indices_dtype
         self.row_alignment = int(row_alignment)
         for E, D, ty in self.specs:
@@ -209,9 +213,10 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
         # the op's overload resolved once and called with positional arguments in
         # schema order: keyword parsing and overload lookup cost more host time per
         # call than the launch itself on small batches
-        op = self._lookup
+        global _LOOKUP
+        op = _LOOKUP
         if op is None:
-            op = self._lookup = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function.default
+            op = _LOOKUP = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function.default
         return op(self.weights_dev, self.weights_uvm, self.weights_placements, self.weights_offsets,
                   self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,
                   self.max_int8_D, self.max_float16_D, self.max_float32_D, indices, offsets,
