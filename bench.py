@@ -51,6 +51,10 @@ def _parse():
     ap.add_argument("--batches", type=int, default=4,
                     help="distinct batches generated before timing and rotated in the timed loop")
     ap.add_argument("--flags", type=int, default=0, help="TBE_FLAG_* tuning switches (C-ABI path)")
+    ap.add_argument("--bag-len", default=None,
+                    help="replace the configuration's bag-length rule (e.g. fixed:33); the batch is scaled so "
+                         "the call keeps the configuration's mean number of lookups (a study of the kernel, "
+                         "not a benchmark configuration)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a plain 1 GiB device copy instead (calibrates rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--traffic", default=None,
@@ -648,7 +652,7 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(),
                           "calls": args.warmup + args.steps}), flush=True)
         return
-    wl = make_workload(args.config, device=dev, num_batches=max(1, args.batches))
+    wl = make_workload(args.config, device=dev, num_batches=max(1, args.batches), bag_len=args.bag_len)
     m = wl.module
     K = len(wl.batches)
     torch.cuda.synchronize()
@@ -747,7 +751,8 @@ def main():
         "dtype": {2: "int8", 3: "int4"}.get(int(m.specs[0][2]), "mixed") if args.config != 3 else "mixed",
         "data": f"synthetic (seeded, generated on device); {K} distinct batches from the same "
                 "distributions, rotated (step s uses batch s % K)",
-        "config": {"workload": f"config{args.config}: {wl.spec.description}",
+        "config": {"workload": f"config{args.config}: {wl.spec.description}" +
+                               (f" with bag_len {args.bag_len} (study, B={wl.spec.B})" if args.bag_len else ""),
                    "tables": len(m.specs), "rows_per_table": m.specs[0][0] if args.config != 3 else "mixed",
                    "D": m.specs[0][1] if args.config != 3 else "mixed", "batch": wl.spec.B,
                    "bag_len": wl.spec.bag_len, "zipf_alpha": wl.spec.zipf_alpha,

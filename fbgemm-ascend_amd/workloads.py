@@ -216,12 +216,27 @@ def make_batch(spec: ConfigSpec, seed: int, device) -> Batch:
     return Batch(indices, offsets, psw, lengths)
 
 
+def mean_bag_len(rule: str) -> float:
+    """Mean bag length of a bag-length rule (the Poisson mean, unclipped)."""
+    kind, *a = rule.split(":")
+    if kind in ("fixed", "poisson"):
+        return float(a[0])
+    if kind == "uniform":
+        return (float(a[0]) + float(a[1])) / 2
+    raise ValueError(rule)
+
+
 def make_workload(cid: int, device="cuda", seed: Optional[int] = None, scale_rows: float = 1.0,
                   batch: Optional[int] = None, table_limit: Optional[int] = None,
-                  num_batches: int = 1) -> Workload:
+                  num_batches: int = 1, bag_len: Optional[str] = None) -> Workload:
     """Tables of configuration `cid` (random weights) and `num_batches` batches of
-    indices drawn from the configuration's distributions (distinct seeds)."""
+    indices drawn from the configuration's distributions (distinct seeds).  bag_len
+    replaces the bag-length rule and scales the batch so the mean number of lookups
+    per call stays the configuration's."""
     spec = config_spec(cid, scale_rows)
+    if bag_len is not None:
+        B = max(1, round(spec.B * mean_bag_len(spec.bag_len) / mean_bag_len(bag_len)))
+        spec = dataclasses.replace(spec, bag_len=bag_len, B=B)
     if batch is not None:
         spec = dataclasses.replace(spec, B=batch)
     if table_limit is not None:
