@@ -564,27 +564,31 @@ def bench_bucketize(args, pkg, dev):
     from _bucketize_cases import CASES, gen_case
 
     case = [c for c in CASES if c.name == "i64_stress"][0]
-    lengths, indices, block_sizes, _ = gen_case(case, 0x7BE5)
-    L_d, I_d, B_d = (torch.from_numpy(a).to(dev) for a in (lengths, indices, block_sizes))
+    # three seeded inputs, rotated call by call: a call does not find its indices in
+    # the memory-side cache because the previous call read the same ones
+    inputs = []
+    for seed in (0x7BE7, 0x7BE6, 0x7BE5):  # 0x7BE5's arrays stay for the sizes and the CPU leg
+        lengths, indices, block_sizes, _ = gen_case(case, seed)
+        inputs.append(tuple(torch.from_numpy(a).to(dev) for a in (lengths, indices, block_sizes)))
     op = torch.ops.fbgemm.block_bucketize_sparse_features
-    step = lambda: op(L_d, I_d, False, False, B_d, case.my_size)  # noqa: E731
-    for _ in range(args.warmup):
-        step()
+    step = lambda i: op(inputs[i % 3][0], inputs[i % 3][1], False, False, inputs[i % 3][2], case.my_size)  # noqa: E731
+    for i in range(args.warmup):
+        step(i)
     stream = torch.cuda.current_stream(dev)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for a, b in evs:
+    for i, (a, b) in enumerate(evs):
         a.record(stream)
-        step()
+        step(i)
         b.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = sorted(a.elapsed_time(b) for a, b in evs)
     per_call_mean = sum(ms) / len(ms)
     # one event pair around all calls (an event pair around each call adds its own gap)
-    mean_ms, _ = time_calls(stream, range(args.steps), lambda i: step())
+    mean_ms, _ = time_calls(stream, range(args.steps), step)
     N, L = indices.size, lengths.size
     nbytes = 2 * N * indices.itemsize + L * lengths.itemsize + case.my_size * L * lengths.itemsize
     cpu = None
@@ -605,7 +609,7 @@ def bench_bucketize(args, pkg, dev):
     out = {"metric": "block_bucketize_sparse_features indices/s, 1 GPU", "value": N / (mean_ms * 1e-3),
            "unit": "indices/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-           "dtype": "int64", "data": "synthetic (seeded)",
+           "dtype": "int64", "data": "synthetic (seeded; 3 inputs rotated)",
            "config": {"workload": "reference perf case i64_stress", "features": case.num_features,
                       "batch": case.batch_size, "lengths": [case.min_length, case.max_length],
                       "my_size": case.my_size, "num_indices": int(N)},

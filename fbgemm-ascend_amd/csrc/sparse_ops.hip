@@ -296,9 +296,15 @@ __device__ __forceinline__ bool map_step(const RowCtx<IT>& c, bool in, std::make
 // waves interleave over it, so the group's waves walk neighbouring rows at the
 // same time (their segments of one bucket are neighbours in the output) and a
 // wave's rows mostly share one feature.
-__device__ __forceinline__ void wave_rows(int64_t L, int64_t& r0, int64_t& r1, int64_t& rs) {
+//
+// The scatter passes `reverse`: its work-groups take the row ranges last to first.
+// The count phase reads the indices roughly first to last (work-groups start in
+// order), so the indices it read last are still in the memory-side cache when the
+// scatter starts on them (i64_stress: 327 -> 322 us with fresh inputs each call).
+__device__ __forceinline__ void wave_rows(int64_t L, int64_t& r0, int64_t& r1, int64_t& rs, bool reverse = false) {
   const int64_t per = (L + gridDim.x - 1) / gridDim.x;
-  const int64_t b0 = std::min<int64_t>(blockIdx.x * per, L);
+  const int64_t bid = reverse ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int64_t b0 = std::min<int64_t>(bid * per, L);
   r0 = b0 + (threadIdx.x >> 6);
   r1 = std::min<int64_t>(b0 + per, L);
   rs = kBBBlock / kWaveBB;
@@ -647,7 +653,7 @@ __global__ __launch_bounds__(kBBBlock) void bb_scatter(BBParams<IT, OT> p) {
   ScatterStage<IT>& st = lds_stage[NB > 0 ? (threadIdx.x >> 6) : 0];
   if constexpr (NB > 0) st.cnt[lane_id()] = 0;
   int64_t r0, r1, rs;
-  wave_rows(p.L, r0, r1, rs);
+  wave_rows(p.L, r0, r1, rs, true);
   for (int64_t g0 = r0; g0 < r1; g0 += kWaveBB * rs) {
     const int64_t rl = g0 + lane_id() * rs;
     const RowCtx<IT> mine = row_ctx_lane(p, rl < r1 ? rl : -1);
