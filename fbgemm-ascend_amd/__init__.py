@@ -11,6 +11,8 @@ The directory name contains a hyphen, so load it with `load_package()` below
 """
 from __future__ import annotations
 
+import importlib.machinery
+import importlib.util
 import os
 
 import torch
@@ -59,6 +61,7 @@ SCHEMAS = [
 
 _schema_libs = []
 _loaded = False
+_ext = None  # _tbe_torch.so imported as a Python extension module (BoundLookup)
 
 
 def _op_defined(qualname: str) -> bool:
@@ -94,6 +97,12 @@ def load_library() -> None:
             "run fbgemm-ascend_amd/build.py (or __graft_entry__.build()) first")
     _define_schema()
     torch.ops.load_library(TORCH_LIB)
+    global _ext
+    name = f"{__name__}._tbe_torch"
+    loader = importlib.machinery.ExtensionFileLoader(name, TORCH_LIB)
+    spec = importlib.util.spec_from_file_location(name, TORCH_LIB, loader=loader)
+    _ext = importlib.util.module_from_spec(spec)
+    loader.exec_module(_ext)
     _loaded = True
 
 

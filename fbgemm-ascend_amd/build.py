@@ -3,7 +3,9 @@
   libtbe_hip.so    hand-written gfx950 kernels + the C ABIs of include/tbe_nbit.h,
                    include/tbe_pooled_ops.h and include/tbe_sparse_ops.h
   _tbe_torch.so    registers fbgemm::int_nbit_split_embedding_codegen_lookup_function
-                   for HIP tensors; links libtbe_hip.so through $ORIGIN
+                   for HIP tensors; links libtbe_hip.so through $ORIGIN; also a Python
+                   extension module (BoundLookup, the module's forward without the
+                   dispatcher)
 
 Both land next to this file so they travel with the source tree.
 """
@@ -12,6 +14,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import sysconfig
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(PKG_DIR)
@@ -94,14 +97,16 @@ def build_torch_binding():
 
     tdir = os.path.dirname(torch.__file__)
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
-           f"-I{INCLUDE}", f"-I{ROCM}/include"]
+           "-DTORCH_EXTENSION_NAME=_tbe_torch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           f"-I{INCLUDE}", f"-I{ROCM}/include", f"-I{sysconfig.get_paths()['include']}"]
     for inc in cpp_extension.include_paths():
         cmd.append(f"-I{inc}")
     cmd += [os.path.join(CSRC, "tbe_torch.cpp"), "-o", TORCH_LIB,
             f"-L{PKG_DIR}", "-ltbe_hip", "-Wl,-rpath,$ORIGIN",
-            f"-L{os.path.join(tdir, 'lib')}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch"]
+            f"-L{os.path.join(tdir, 'lib')}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch",
+            "-ltorch_python"]
     _run(cmd)
 
 

@@ -16,6 +16,7 @@
 #include <ATen/ATen.h>
 #include <ATen/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
 #include <torch/library.h>
 
 #include <limits>
@@ -432,7 +433,54 @@ block_bucketize_sparse_features_hip(const Tensor& lengths, const Tensor& indices
   return {new_lengths, new_indices, opt(new_w), opt(new_pos), opt(unb)};
 }
 
+// The module's forward without the dispatcher: the operator's arguments that do not
+// change between calls (the module's buffers and sizes) are bound once, and a call
+// passes only indices, offsets and per-sample weights.  Same function, checks and
+// plan cache as the operator; what it saves is the Python-side packing of 23
+// arguments into the dispatcher's boxed form (most of the host time of a call on a
+// small batch).
+struct BoundLookup {
+  Tensor dev_weights, uvm_weights, weights_placements, weights_offsets, weights_tys, D_offsets;
+  int64_t total_D, max_int2_D, max_int4_D, max_int8_D, max_float16_D, max_float32_D, pooling_mode, output_dtype;
+  std::optional<int64_t> row_alignment, max_float8_D, fp8_exponent_bits, fp8_exponent_bias;
+
+  Tensor operator()(const Tensor& indices, const Tensor& offsets, const std::optional<Tensor>& indice_weights) const {
+    // the dispatcher would pick a backend from the tensors' devices: with none on a
+    // HIP device there is no implementation (no CPU fallback), as through the op
+    TORCH_CHECK_NOT_IMPLEMENTED(
+        dev_weights.is_cuda() || indices.is_cuda() || offsets.is_cuda() ||
+            (indice_weights && indice_weights->is_cuda()),
+        "Could not run 'fbgemm::int_nbit_split_embedding_codegen_lookup_function' with arguments from the '",
+        indices.device().type(), "' backend: this package implements it for HIP tensors only");
+    return int_nbit_split_embedding_codegen_lookup_function_hip(
+        dev_weights, uvm_weights, weights_placements, weights_offsets, weights_tys, D_offsets, total_D,
+        max_int2_D, max_int4_D, max_int8_D, max_float16_D, max_float32_D, indices, offsets, pooling_mode,
+        indice_weights, output_dtype, std::nullopt, std::nullopt, row_alignment, max_float8_D, fp8_exponent_bits,
+        fp8_exponent_bias);
+  }
+};
+
 }  // namespace tbe_torch
+
+PYBIND11_MODULE(_tbe_torch, m) {
+  namespace py = pybind11;
+  using at::Tensor;
+  py::class_<tbe_torch::BoundLookup>(m, "BoundLookup")
+      .def(py::init([](Tensor dev_weights, Tensor uvm_weights, Tensor weights_placements, Tensor weights_offsets,
+                       Tensor weights_tys, Tensor D_offsets, int64_t total_D, int64_t max_int2_D,
+                       int64_t max_int4_D, int64_t max_int8_D, int64_t max_float16_D, int64_t max_float32_D,
+                       int64_t pooling_mode, int64_t output_dtype, std::optional<int64_t> row_alignment,
+                       std::optional<int64_t> max_float8_D, std::optional<int64_t> fp8_exponent_bits,
+                       std::optional<int64_t> fp8_exponent_bias) {
+             return tbe_torch::BoundLookup{dev_weights, uvm_weights, weights_placements, weights_offsets,
+                                           weights_tys, D_offsets, total_D, max_int2_D, max_int4_D,
+                                           max_int8_D, max_float16_D, max_float32_D, pooling_mode,
+                                           output_dtype, row_alignment, max_float8_D, fp8_exponent_bits,
+                                           fp8_exponent_bias};
+           }))
+      .def("__call__", &tbe_torch::BoundLookup::operator(), py::arg("indices"), py::arg("offsets"),
+           py::arg("indice_weights") = py::none());
+}
 
 // PyTorch-ROCm routes HIP tensors through the CUDA dispatch key.
 TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {

@@ -68,9 +68,11 @@ def _spec_fields(spec) -> Tuple[int, int, SparseType]:
     return int(E), int(D), SparseType(int(ty))
 
 
-# The lookup op's default overload, resolved at the first forward (the op is registered
-# when the package is imported; a module-level cache keeps modules picklable).
-_LOOKUP = None
+# Attributes bound into the module's BoundLookup: setting one drops the binding.
+_BOUND_FIELDS = frozenset((
+    "weights_dev", "weights_uvm", "weights_placements", "weights_offsets", "weights_tys", "D_offsets",
+    "total_D", "max_int2_D", "max_int4_D", "max_int8_D", "max_float16_D", "max_float32_D", "max_float8_D",
+    "pooling_mode", "output_dtype", "row_alignment", "fp8_exponent_bits", "fp8_exponent_bias"))
 
 
 class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
@@ -208,17 +210,39 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
         sb.copy_(torch.stack([scale, bias], 1).contiguous().view(torch.uint8).view(E, 4))
 
     # ------------------------------------------------------------------ forward
+    def _bind(self):
+        """The op's arguments that do not change between calls, bound once in C++
+        (`BoundLookup`): a forward then passes three arguments instead of packing
+        23 into the dispatcher's boxed form, which costs more host time than the
+        launch itself on small batches.  Same function, checks and plan cache as
+        torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function."""
+        from . import _ext
+        b = _ext.BoundLookup(self.weights_dev, self.weights_uvm, self.weights_placements, self.weights_offsets,
+                             self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,
+                             self.max_int8_D, self.max_float16_D, self.max_float32_D, int(self.pooling_mode),
+                             self.output_dtype, self.row_alignment, self.max_float8_D, self.fp8_exponent_bits,
+                             self.fp8_exponent_bias)
+        self.__dict__["_bound"] = b
+        return b
+
+    def __setattr__(self, name, value):
+        if name in _BOUND_FIELDS:
+            self.__dict__["_bound"] = None
+        super().__setattr__(name, value)
+
+    def _apply(self, fn, *args, **kwargs):
+        # .to() / .cuda() / .half() may replace the buffers
+        self.__dict__["_bound"] = None
+        return super()._apply(fn, *args, **kwargs)
+
+    def __getstate__(self):
+        state = self.__dict__.copy()
+        state["_bound"] = None  # a C++ object: rebuilt at the first forward
+        return state
+
     def forward(self, indices: torch.Tensor, offsets: torch.Tensor,
                 per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
-        # the op's overload resolved once and called with positional arguments in
-        # schema order: keyword parsing and overload lookup cost more host time per
-        # call than the launch itself on small batches
-        global _LOOKUP
-        op = _LOOKUP
-        if op is None:
-            op = _LOOKUP = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function.default
-        return op(self.weights_dev, self.weights_uvm, self.weights_placements, self.weights_offsets,
-                  self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,
-                  self.max_int8_D, self.max_float16_D, self.max_float32_D, indices, offsets,
-                  int(self.pooling_mode), per_sample_weights, self.output_dtype, None, None, self.row_alignment,
-                  self.max_float8_D, self.fp8_exponent_bits, self.fp8_exponent_bias)
+        b = self.__dict__.get("_bound")
+        if b is None:
+            b = self._bind()
+        return b(indices, offsets, per_sample_weights)

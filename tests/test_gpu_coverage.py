@@ -449,3 +449,47 @@ def test_packer_float_to_op(pkg, oracle, gpu, ty, pm, weighted):
         assert bool((err <= bound * (1 + 1e-6) + 1e-5 * (mag + ref_f.abs())).all()), f"table {t} vs float"
         # the quantisation is not a no-op: the bound is tight enough to matter
         assert float(err.max()) > 0
+
+
+# ----------------------------------------------------------------- the module's bound forward
+
+def _op_call(m, idx, off, psw):
+    return torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(
+        dev_weights=m.weights_dev, uvm_weights=m.weights_uvm, weights_placements=m.weights_placements,
+        weights_offsets=m.weights_offsets, weights_tys=m.weights_tys, D_offsets=m.D_offsets,
+        total_D=m.total_D, max_int2_D=m.max_int2_D, max_int4_D=m.max_int4_D, max_int8_D=m.max_int8_D,
+        max_float16_D=m.max_float16_D, max_float32_D=m.max_float32_D, indices=idx, offsets=off,
+        pooling_mode=int(m.pooling_mode), indice_weights=psw, output_dtype=m.output_dtype,
+        lxu_cache_weights=None, lxu_cache_locations=None, row_alignment=m.row_alignment,
+        max_float8_D=m.max_float8_D, fp8_exponent_bits=m.fp8_exponent_bits,
+        fp8_exponent_bias=m.fp8_exponent_bias)
+
+
+@pytest.mark.parametrize("ty,pm,weighted,out_ty", [(INT4, 0, False, FP16), (INT8, 1, True, FP32),
+                                                   (FP8, 2, False, BF16), (INT2, 0, True, FP32)])
+def test_module_forward_equals_op(pkg, gpu, ty, pm, weighted, out_ty):
+    """The module's forward (its bound C++ call) returns the op's output bit for bit."""
+    m, idx, off, psw = _random_case(pkg, gpu, 77, 3, ty, pm, weighted, torch.int32, out_ty, B=32, L=40)
+    got, want = m(idx, off, psw), _op_call(m, idx, off, psw)
+    torch.cuda.synchronize()
+    assert got.dtype == want.dtype and got.shape == want.shape
+    assert torch.equal(got, want)
+
+
+def test_module_rebinds_after_changes(pkg, gpu):
+    """Attribute writes, buffer replacement and .to() drop the bound call; the next
+    forward follows the module's current state."""
+    m, idx, off, _ = _random_case(pkg, gpu, 78, 2, INT8, 0, False, torch.int64, FP16, B=16, L=20)
+    first = m(idx, off)
+    assert first.dtype == torch.float16
+    m.output_dtype = FP32
+    second = m(idx, off)
+    assert second.dtype == torch.float32
+    assert torch.equal(second, _op_call(m, idx, off, None))
+    m.weights_dev = torch.zeros_like(m.weights_dev)  # every row: scale 0, bias 0
+    assert torch.count_nonzero(m(idx, off)) == 0
+    m.fill_random_weights(5)  # in place: same tensor, bound call kept
+    assert torch.equal(m(idx, off), _op_call(m, idx, off, None))
+    m = m.to(gpu)
+    assert torch.equal(m(idx, off), _op_call(m, idx, off, None))
+    torch.cuda.synchronize()

@@ -399,3 +399,20 @@ def _stride(ty, D, align):
     bits = {FP32: 32, FP16: 16, BF16: 16, FP8: 8, INT8: 8, INT4: 4, INT2: 2}[ty]
     u = D * bits // 8 + (4 if ty in (INT8, INT4, INT2) else 0)
     return (u + align - 1) // align * align
+
+
+def test_module_copies_drop_the_bound_call(pkg):
+    """deepcopy / pickle of the module work (the bound C++ call is not copied) and the
+    copy still refuses CPU tensors like the op."""
+    import copy
+    import pickle
+    from fbgemm_ascend_amd import IntNBitTableBatchedEmbeddingBagsCodegen, SparseType
+    m = IntNBitTableBatchedEmbeddingBagsCodegen([(10, 16, SparseType.INT8)], device="cpu")
+    idx, off = torch.tensor([1, 2], dtype=torch.int32), torch.tensor([0, 2], dtype=torch.int32)
+    with pytest.raises(NotImplementedError):
+        m(idx, off)
+    for c in (copy.deepcopy(m), pickle.loads(pickle.dumps(m))):
+        assert c.__dict__.get("_bound") is None
+        assert torch.equal(c.weights_offsets, m.weights_offsets)
+        with pytest.raises(NotImplementedError):
+            c(idx, off)
