@@ -57,7 +57,8 @@ struct BBParams {
   float* __restrict__ new_weights;
   IT* __restrict__ new_pos;
   IT* __restrict__ unb;
-  uint32_t* __restrict__ done;  // [my_size * L] write cursors of the scatter
+  uint32_t* __restrict__ done;  // [my_size * L] write cursors of the scatter (my_size > 64)
+  uint8_t* __restrict__ slow;   // [L] my_size <= 64: rows the scatter maps with the general code
   int64_t L;
   int64_t N;
   int64_t my_size;
@@ -276,10 +277,19 @@ __device__ __forceinline__ bool map_index(const RowCtx<IT>& c, std::make_unsigne
 // For rows marked fast, when no lane of the wave holds an index at or above
 // gsize (the wave-uniform common case), bucket = u / lsize and new index
 // u % lsize by the 32-bit multiply-shift division, without branches; otherwise
-// the general map_index.
-template <bool FAST, typename IT>
+// the general map_index.  ONLY_FAST: the caller has checked that every index of
+// the step is below gsize, so the general code is not compiled in (it costs the
+// scatter ~17 VGPRs and ~8 % of its time).
+template <bool FAST, typename IT, bool ONLY_FAST = false>
 __device__ __forceinline__ bool map_step(const RowCtx<IT>& c, bool in, std::make_unsigned_t<IT> u, uint64_t my,
                                          bool keep, int64_t& bucket, IT& nidx) {
+  if constexpr (ONLY_FAST) {
+    const uint32_t n = static_cast<uint32_t>(u);
+    const uint32_t q = c.dl.div(n);
+    bucket = static_cast<int64_t>(q);
+    nidx = keep ? static_cast<IT>(u) : static_cast<IT>(n - q * c.dl.d);
+    return in && q < my;
+  }
   if constexpr (FAST) {
     if (__builtin_amdgcn_ballot_w64(in && !(u < c.gsize)) == 0) {
       const uint32_t n = static_cast<uint32_t>(u);
@@ -528,8 +538,13 @@ __device__ __forceinline__ uint32_t wave_exclusive_scan(uint32_t x) {
   return s - x;
 }
 
-template <bool FAST, int NB, typename IT, typename OT>
-__device__ __forceinline__ void scatter_row_staged(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r,
+//
+// ONLY_FAST (rows marked fast): gives up on the row, returning false, at the
+// first chunk holding an index at or above gsize, before writing anything of that
+// chunk; the general pass then rewrites the whole row (the same values at the same
+// positions).  Returns true when the row is done.
+template <bool FAST, int NB, typename IT, typename OT, bool ONLY_FAST = false>
+__device__ __forceinline__ bool scatter_row_staged(const BBParams<IT, OT>& p, const RowCtx<IT>& c, int64_t r,
                                                    ScatterStage<IT>& st) {
   using UIT = std::make_unsigned_t<IT>;
   constexpr uint32_t kNone = 0xFFu;
@@ -542,6 +557,12 @@ __device__ __forceinline__ void scatter_row_staged(const BBParams<IT, OT>& p, co
       uk[k] = idx[std::min<int64_t>(chunk + k * kWaveBB + lane, c.e - 1)];
     // the row's cursors, loaded with its first indices (one wait for both)
     if (chunk == c.s && lane < p.my_size) st.cur[lane] = static_cast<int64_t>(p.new_offsets[lane * p.L + r]);
+    if constexpr (ONLY_FAST) {
+      bool high = false;
+#pragma unroll
+      for (int k = 0; k < kChunk; ++k) high |= chunk + k * kWaveBB + lane < c.e && !(uk[k] < c.gsize);
+      if (__builtin_amdgcn_ballot_w64(high) != 0) return false;
+    }
     // 1. map and count
     uint32_t bk[kChunk];
     IT vk[kChunk];
@@ -553,7 +574,7 @@ __device__ __forceinline__ void scatter_row_staged(const BBParams<IT, OT>& p, co
       if (base < c.e) {
         int64_t b = 0;
         IT v = 0;
-        if (map_step<FAST, IT>(c, base + lane < c.e, uk[k], p.my_size, p.keep, b, v)) {
+        if (map_step<FAST, IT, ONLY_FAST>(c, base + lane < c.e, uk[k], p.my_size, p.keep, b, v)) {
           bk[k] = static_cast<uint32_t>(b);
           vk[k] = v;
           atomicAdd(&st.cnt[b], 1u);
@@ -601,6 +622,7 @@ __device__ __forceinline__ void scatter_row_staged(const BBParams<IT, OT>& p, co
     }
     st.cnt[lane] = 0;
   }
+  return true;
 }
 
 template <bool FAST, typename IT, typename OT>
@@ -647,20 +669,54 @@ __device__ __forceinline__ void scatter_row_atomic(const BBParams<IT, OT>& p, co
   }
 }
 
-template <typename IT, typename OT, int NB>
+// PASS (my_size <= 64): 1 takes every row marked fast with the fast map only and
+// flags (`slow`, one byte per row) the rows it leaves: those not marked fast and
+// those holding an index at or above gsize; 2 takes the flagged rows with the
+// general map.  Two kernels, so the general map's registers do not limit the fast
+// pass.  my_size > 64: PASS 0, every row.
+template <typename IT, typename OT, int NB, int PASS>
 __global__ __launch_bounds__(kBBBlock) void bb_scatter(BBParams<IT, OT> p) {
   __shared__ ScatterStage<IT> lds_stage[NB > 0 ? kBBBlock / kWaveBB : 1];
   ScatterStage<IT>& st = lds_stage[NB > 0 ? (threadIdx.x >> 6) : 0];
   if constexpr (NB > 0) st.cnt[lane_id()] = 0;
   int64_t r0, r1, rs;
+  if constexpr (PASS == 2) {
+    // few rows if any: each wave checks 64 consecutive rows' flags at a time
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * (kBBBlock / kWaveBB);
+    r0 = (static_cast<int64_t>(blockIdx.x) * (kBBBlock / kWaveBB) + (threadIdx.x >> 6)) * kWaveBB;
+    r1 = p.L;
+    rs = 1;
+    for (int64_t g0 = r0; g0 < r1; g0 += waves * kWaveBB) {
+      const int64_t rl = g0 + lane_id();
+      uint64_t take = __builtin_amdgcn_ballot_w64(rl < r1 && p.slow[rl] != 0);
+      if (take == 0) continue;  // wave-uniform
+      const RowCtx<IT> mine = row_ctx_lane(p, rl < r1 ? rl : -1);
+      while (take) {
+        const int j = __builtin_ctzll(take);
+        take &= take - 1;
+        const RowCtx<IT> c = row_ctx_of(mine, j);
+        if (!c.ok) continue;
+        if (c.fast) scatter_row_staged<true, NB>(p, c, g0 + j, st);
+        else scatter_row_staged<false, NB>(p, c, g0 + j, st);
+      }
+    }
+    return;
+  }
   wave_rows(p.L, r0, r1, rs, true);
   for (int64_t g0 = r0; g0 < r1; g0 += kWaveBB * rs) {
     const int64_t rl = g0 + lane_id() * rs;
+    uint64_t take = __builtin_amdgcn_ballot_w64(rl < r1);
     const RowCtx<IT> mine = row_ctx_lane(p, rl < r1 ? rl : -1);
-    const int nrows = static_cast<int>(std::min<int64_t>(kWaveBB, (r1 - g0 + rs - 1) / rs));
-    for (int j = 0; j < nrows; ++j) {
+    while (take) {
+      const int j = __builtin_ctzll(take);
+      take &= take - 1;
       const int64_t r = g0 + j * rs;
       const RowCtx<IT> c = row_ctx_of(mine, j);
+      if constexpr (PASS == 1) {
+        const bool done = !c.ok || (c.fast && scatter_row_staged<true, NB, IT, OT, true>(p, c, r, st));
+        if (lane_id() == 0) p.slow[r] = done ? 0 : 1;
+        continue;
+      }
       if (!c.ok) continue;
       if constexpr (NB > 0) {
         if (c.fast) scatter_row_staged<true, NB>(p, c, r, st);
@@ -795,7 +851,8 @@ __global__ __launch_bounds__(kBBBlock) void scan_tiles_based(const T* __restrict
 int64_t scan_tiles_of(int64_t n) { return (n + kScanTile - 1) / kScanTile; }
 
 int64_t ws_layout(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
-  // [done: my*L uint32][pad to 256][tile sums: tiles * os]
+  // [done: my*L uint32 (my_size <= 64: the first L bytes hold the row flags)][pad to 256]
+  // [tile sums: tiles * os]
   const int64_t done_bytes = my * L * 4;
   const int64_t so = (done_bytes + 255) / 256 * 256;
   if (sums_off) *sums_off = so;
@@ -852,10 +909,11 @@ NoAllocDevice* noalloc_device() {
   return &d;
 }
 
-// Scratch bytes a call needs: the per-segment write cursors (my_size > 64 only;
-// up to 64 buckets the cursors live in registers and LDS) and the scan's tile sums.
+// Scratch bytes a call needs: the per-segment write cursors (my_size > 64; up to 64
+// buckets the cursors live in registers and LDS, and the region holds the count
+// phase's one-byte row flags instead) and the scan's tile sums.
 int64_t noalloc_need(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
-  const int64_t done_bytes = my > kWaveBB ? (my * L * 4 + 255) / 256 * 256 : 0;
+  const int64_t done_bytes = ((my > kWaveBB ? my * L * 4 : L) + 255) / 256 * 256;
   if (sums_off) *sums_off = done_bytes;
   return done_bytes + std::max<int64_t>(1, scan_tiles_of(my * L)) * os;
 }
@@ -878,6 +936,7 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_of
   p.new_pos = static_cast<IT*>(a->new_pos);
   p.unb = static_cast<IT*>(a->unbucketize_permute);
   p.done = static_cast<uint32_t*>(ws);
+  p.slow = static_cast<uint8_t*>(ws);  // my_size <= 64 only, where the cursors are not used
   OT* sums = reinterpret_cast<OT*>(static_cast<uint8_t*>(ws) + sums_off);
   p.L = a->lengths_size;
   p.N = a->num_indices;
@@ -918,9 +977,17 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_of
   }
   if (p.N > 0) {
     const dim3 g(static_cast<uint32_t>(row_blocks));
-    if (!reg) hipLaunchKernelGGL((bb_scatter<IT, OT, 0>), g, dim3(kBBBlock), 0, s, p);
-    else if (nbits <= 4) hipLaunchKernelGGL((bb_scatter<IT, OT, 4>), g, dim3(kBBBlock), 0, s, p);
-    else hipLaunchKernelGGL((bb_scatter<IT, OT, 6>), g, dim3(kBBBlock), 0, s, p);
+    // the general pass: one wave per 64 rows, at most one block per CU
+    const dim3 g2(static_cast<uint32_t>(std::min<int64_t>(std::max<int64_t>(1, (p.L + 255) / 256), cus)));
+    if (!reg) {
+      hipLaunchKernelGGL((bb_scatter<IT, OT, 0, 0>), g, dim3(kBBBlock), 0, s, p);
+    } else if (nbits <= 4) {
+      hipLaunchKernelGGL((bb_scatter<IT, OT, 4, 1>), g, dim3(kBBBlock), 0, s, p);
+      hipLaunchKernelGGL((bb_scatter<IT, OT, 4, 2>), g2, dim3(kBBBlock), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((bb_scatter<IT, OT, 6, 1>), g, dim3(kBBBlock), 0, s, p);
+      hipLaunchKernelGGL((bb_scatter<IT, OT, 6, 2>), g2, dim3(kBBBlock), 0, s, p);
+    }
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(TBE_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));

@@ -88,11 +88,12 @@ int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* args, void*
  * under HIP graph capture, tight serving loops, harnesses that forbid it).  The
  * caller still passes every input and output.
  *
- * Scratch (the per-segment write cursors when my_size > 64, and the scan's tile
- * sums) lives in a static device array of TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES
- * bytes that each GPU the library runs on holds until the process ends; it is
- * cleared by the call's own kernels where it must start at zero.  A call needs
- *   (my_size > 64 ? roundup(4 * my_size * lengths_size, 256) : 0)
+ * Scratch (the per-segment write cursors when my_size > 64, one flag byte per
+ * row otherwise, and the scan's tile sums) lives in a static device array of
+ * TBE_BLOCK_BUCKETIZE_NOALLOC_SCRATCH_BYTES bytes that each GPU the library runs
+ * on holds until the process ends; it is cleared or fully written by the call's own
+ * kernels where it must start at a known value.  A call needs
+ *   roundup(my_size > 64 ? 4 * my_size * lengths_size : lengths_size, 256)
  *   + offset_size * max(1, ceil(my_size * lengths_size / 1024))
  * bytes of it; larger calls are rejected with TBE_ERR_UNSUPPORTED and a message.
  * Every call on one GPU shares that GPU's array, so calls on one GPU are made

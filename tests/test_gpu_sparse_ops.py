@@ -179,6 +179,31 @@ def test_bucketize_indices_beyond_blocks(pkg, oracle, gpu, dtype, my_size, tnb):
 
 
 @pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("my_size", [16, 40])
+@pytest.mark.parametrize("at", [5, 600, 1500])
+def test_bucketize_high_index_in_one_chunk(pkg, oracle, gpu, dtype, my_size, at):
+    # rows of 400-1800 indices, every third one with a single index at or above the
+    # blocks at position `at`: the fast scatter pass writes the chunks before it,
+    # gives the row up at that chunk, and the general pass rewrites the whole row
+    from _bucketize_cases import Case
+    case = Case(f"high_at{at}_my{my_size}", 4, 12, 400, 1800, 8, 40, my_size, dtype)
+    for seed, kw in ((51, dict(weights=True, sequence=True)), (52, dict(sequence=True, keep=True)),
+                     (53, dict(weights=True, bucketize_pos=True))):
+        lengths = gen_case(case, seed, kw.get("weights", False))[0]
+        off = np.concatenate([[0], np.cumsum(lengths)])
+
+        def mutate(ix, lengths=lengths, off=off):
+            ix = ix.copy()
+            hi = np.iinfo(ix.dtype).max
+            for r in range(0, lengths.size, 3):
+                if lengths[r] > at:
+                    ix[off[r] + at] = hi - r
+            return ix
+
+        _check(oracle, gpu, case, seed, mutate=mutate, **kw)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
 @pytest.mark.parametrize("my_size", [5, 100])
 def test_bucketize_bucket_past_my_size_dropped(pkg, oracle, gpu, dtype, my_size):
     # total_num_blocks not a multiple of my_size and indices at or above the
