@@ -230,6 +230,11 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(torch.nn.Module):
             self.__dict__["_bound"] = None
         super().__setattr__(name, value)
 
+    def register_buffer(self, name, tensor, persistent=True):
+        if name in _BOUND_FIELDS:
+            self.__dict__["_bound"] = None
+        super().register_buffer(name, tensor, persistent)
+
     def _apply(self, fn, *args, **kwargs):
         # .to() / .cuda() / .half() may replace the buffers
         self.__dict__["_bound"] = None

@@ -492,4 +492,6 @@ def test_module_rebinds_after_changes(pkg, gpu):
     assert torch.equal(m(idx, off), _op_call(m, idx, off, None))
     m = m.to(gpu)
     assert torch.equal(m(idx, off), _op_call(m, idx, off, None))
+    m.register_buffer("weights_dev", torch.zeros_like(m.weights_dev))
+    assert torch.count_nonzero(m(idx, off)) == 0
     torch.cuda.synchronize()
