@@ -95,6 +95,10 @@ def run_oracle(oracle, prob, pooling_mode, output_dtype, row_alignment=16):
                           row_alignment=row_alignment, fp8_exponent_bits=bits, fp8_exponent_bias=bias)
 
 
+F16_MAX = 65504.0         # largest finite half
+F16_INF_FROM = 65520.0    # half-way to the next power of two: RNE rounds here and above to inf
+
+
 def bag_tolerance(prob, pooling_mode, output_dtype):
     """atol per output element [B', total_D]."""
     rtol = RTOL[output_dtype]
@@ -131,9 +135,22 @@ def assert_bag_parity(gpu_out, prob, ref32, pooling_mode, output_dtype, label=""
     else:
         atol = bag_tolerance(prob, pooling_mode, output_dtype)
         rtol = RTOL[output_dtype]
-    err = np.abs(got.astype(np.float64) - ref32.astype(np.float64))
-    lim = atol + rtol * np.abs(ref32.astype(np.float64))
+    r64 = ref32.astype(np.float64)
+    err = np.abs(got.astype(np.float64) - r64)
+    lim = atol + rtol * np.abs(r64)
     bad = err > lim
+    if output_dtype == 1:
+        # fp16 out: the round-to-nearest-even cast (P:330) takes sums from 65520 up to
+        # +-inf and sums from 65504 to 65520 to +-65504; near those bounds the fp32
+        # summation order may land on either side
+        a = np.abs(r64)
+        same_sign = np.sign(got) == np.sign(r64)
+        must_inf = a >= F16_INF_FROM * (1 + rtol)
+        near = a >= F16_MAX * (1 - rtol)
+        edge_ok = near & ~must_inf & same_sign & (np.isinf(got) | (np.abs(got) >= F16_MAX * (1 - rtol)))
+        inf_ok = must_inf & same_sign & np.isinf(got)
+        bad = (bad & ~edge_ok & ~inf_ok) | (must_inf & ~inf_ok)
+        err = np.where(edge_ok | inf_ok, 0.0, err)
     if bad.any():
         i = np.argwhere(bad)[0]
         raise AssertionError(

@@ -416,3 +416,20 @@ def test_module_copies_drop_the_bound_call(pkg):
         assert torch.equal(c.weights_offsets, m.weights_offsets)
         with pytest.raises(NotImplementedError):
             c(idx, off)
+
+
+def test_parity_fp16_overflow_rule():
+    """The fp16 comparison accepts +-inf exactly where the RNE cast of the fp32 sum
+    overflows, and nowhere else."""
+    import numpy as np
+    from _parity import assert_bag_parity
+    prob = {"weights_tys": np.array([1], np.uint8), "B": 1, "D_offsets": np.array([0, 4]),
+            "indices": np.array([0]), "offsets": np.array([0, 1]), "psw": None,
+            "rowmax": [np.array([1.0])]}
+    ref = np.array([[70000.0, -80000.0, 65510.0, 100.0]], np.float32)
+    ok = torch.tensor([[float("inf"), float("-inf"), 65504.0, 100.0]], dtype=torch.float16)
+    assert_bag_parity(ok, prob, ref, 0, 1)
+    for bad in ([65504.0, float("-inf"), 65504.0, 100.0], [float("-inf"), float("-inf"), 65504.0, 100.0],
+                [float("inf"), float("-inf"), 65504.0, float("inf")]):
+        with pytest.raises(AssertionError):
+            assert_bag_parity(torch.tensor([bad], dtype=torch.float16), prob, ref, 0, 1)
