@@ -69,3 +69,34 @@ def test_random_mixed_modules(pkg, oracle, gpu, seed):
     if idx.numel() == 0:
         pytest.skip("no lookups (the op requires at least one index, A:117)")
     _check_module(oracle, m, idx, off, psw, label, flags=flags)
+
+
+# ----------------------------------------------------------------- block_bucketize
+
+@pytest.mark.parametrize("seed", range(120))
+def test_random_bucketize(pkg, oracle, gpu, seed):
+    """Random shapes and options of block_bucketize_sparse_features against the oracle:
+    my_size on both sides of 64 (LDS and memory counters), rows from empty to several
+    512-index chunks, optional total_num_blocks, batch_size_per_feature, position
+    lists, weights, sequence, keep_orig_idx, and indices past the blocks (the general
+    index map, in the general scatter pass)."""
+    import numpy as np
+    from _bucketize_cases import Case
+    from test_gpu_sparse_ops import _beyond_blocks, _check
+    rnd = random.Random(0xB0C4 + seed)
+    dtype = rnd.choice([np.int32, np.int64])
+    my = rnd.choice([1, 2, 3, 5, 16, 33, 63, 64, 65, 100])
+    lo = rnd.choice([0, 0, 4, 100])
+    hi = lo + rnd.choice([3, 30, 300, 900])
+    case = Case(f"fuzz{seed}", rnd.randint(1, 12), rnd.randint(1, 96), lo, hi, 1, rnd.randint(1, 64), my, dtype)
+    tnb = rnd.choice([None, None, "multiple", "rand"])
+    pos = rnd.random() < 0.25
+    # indices past a feature's blocks (put there on purpose, or by batch_size_per_feature
+    # giving a row to a feature with smaller blocks than the one its indices were drawn
+    # for) are left out when total_num_blocks is not a multiple of my_size, and the
+    # output tail past the kept ones is then unwritten: that case has its own test
+    # (test_bucketize_bucket_past_my_size_dropped), so "rand" goes without them here
+    bspf = tnb != "rand" and not pos and rnd.random() < 0.25
+    mutate = _beyond_blocks(dtype, my) if (tnb != "rand" and not pos and rnd.random() < 0.3) else None
+    _check(oracle, gpu, case, seed, weights=rnd.random() < 0.5, bucketize_pos=rnd.random() < 0.5,
+           sequence=rnd.random() < 0.5, keep=rnd.random() < 0.3, tnb=tnb, bspf=bspf, pos=pos, mutate=mutate)
