@@ -94,7 +94,7 @@ class TbeBlockBucketizeArgs(ctypes.Structure):
                 ("new_offsets", ctypes.c_void_p), ("new_indices", ctypes.c_void_p),
                 ("new_weights", ctypes.c_void_p), ("new_pos", ctypes.c_void_p),
                 ("unbucketize_permute", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
-                ("workspace_bytes", ctypes.c_int64)]
+                ("workspace_bytes", ctypes.c_int64), ("lengths", ctypes.c_void_p)]
 
 
 _lib = None
@@ -266,18 +266,21 @@ def permute_pooled_embs(pooled_embs, offset_dim_list, permute_list, inv_offset_d
 
 def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, block_sizes, my_size,
                                     weights=None, batch_size_per_feature=None, block_bucketize_pos=None,
-                                    keep_orig_idx=False, total_num_blocks=None, noalloc=False, sync=True):
+                                    keep_orig_idx=False, total_num_blocks=None, noalloc=False, sync=True,
+                                    pass_offsets=True):
     """tbe_block_bucketize_sparse_features on torch device tensors; returns the op's
     five outputs (None where not requested) plus new_offsets.  noalloc=True calls
     tbe_block_bucketize_sparse_features_noalloc instead (no workspace passed).
     sync=False returns without waiting for the launches (the temporaries the call
-    reads are kept alive by new_offsets until it is freed)."""
+    reads are kept alive by new_offsets until it is freed).  pass_offsets=False hands
+    the lengths to the library instead of their cumsum (the torch op's way)."""
     import torch
 
     dev = indices.device
     L, N, F = lengths.numel(), indices.numel(), block_sizes.numel()
     lopt = dict(dtype=lengths.dtype, device=dev)
-    offsets = torch.cumsum(lengths, 0, dtype=lengths.dtype).contiguous()
+    lengths = lengths.contiguous()
+    offsets = torch.cumsum(lengths, 0, dtype=lengths.dtype).contiguous() if pass_offsets else None
     bso = None
     if batch_size_per_feature is not None:
         bso = torch.cat([torch.zeros(1, **lopt),
@@ -288,7 +291,7 @@ def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, b
     new_w = torch.empty(N, dtype=torch.float32, device=dev) if weights is not None else None
     new_pos = torch.empty_like(new_indices) if bucketize_pos else None
     unb = torch.empty_like(new_indices) if sequence else None
-    keep = [offsets, bso]
+    keep = [offsets, bso, lengths]
     pos_ptrs = pos_lens = None
     if block_bucketize_pos is not None:
         ps = [p.contiguous() for p in block_bucketize_pos]
@@ -307,6 +310,7 @@ def block_bucketize_sparse_features(lengths, indices, bucketize_pos, sequence, b
     a.new_lengths, a.new_offsets, a.new_indices = ptr(new_lengths), ptr(new_offsets), ptr(new_indices)
     a.new_weights, a.new_pos, a.unbucketize_permute = ptr(new_w), ptr(new_pos), ptr(unb)
     a.workspace, a.workspace_bytes = ptr(ws), wsb
+    a.lengths = ptr(lengths)
     stream = torch.cuda.current_stream(dev).cuda_stream if indices.is_cuda else 0
     fn = lib().tbe_block_bucketize_sparse_features_noalloc if noalloc else lib().tbe_block_bucketize_sparse_features
     rc = fn(ctypes.byref(a), ctypes.c_void_p(stream))

@@ -850,11 +850,15 @@ __global__ __launch_bounds__(kBBBlock) void scan_tiles_based(const T* __restrict
 
 int64_t scan_tiles_of(int64_t n) { return (n + kScanTile - 1) / kScanTile; }
 
+// Bytes of the row offsets the library forms when the caller passes lengths only:
+// the complete cumsum, L + 1 elements.
+int64_t offsets_bytes(int64_t L, int32_t os) { return ((L + 1) * os + 255) / 256 * 256; }
+
 int64_t ws_layout(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
   // [done: my*L uint32 (my_size <= 64: the first L bytes hold the row flags)][pad to 256]
-  // [tile sums: tiles * os]
+  // [row offsets: (L + 1) * os][pad to 256][tile sums: tiles * os]
   const int64_t done_bytes = my * L * 4;
-  const int64_t so = (done_bytes + 255) / 256 * 256;
+  const int64_t so = (done_bytes + 255) / 256 * 256 + offsets_bytes(L, os);
   if (sums_off) *sums_off = so;
   return so + std::max<int64_t>(1, scan_tiles_of(my * L)) * os;
 }
@@ -911,9 +915,10 @@ NoAllocDevice* noalloc_device() {
 
 // Scratch bytes a call needs: the per-segment write cursors (my_size > 64; up to 64
 // buckets the cursors live in registers and LDS, and the region holds the count
-// phase's one-byte row flags instead) and the scan's tile sums.
+// phase's one-byte row flags instead), the row offsets formed from lengths, and the
+// scan's tile sums.
 int64_t noalloc_need(int64_t my, int64_t L, int32_t os, int64_t* sums_off) {
-  const int64_t done_bytes = ((my > kWaveBB ? my * L * 4 : L) + 255) / 256 * 256;
+  const int64_t done_bytes = ((my > kWaveBB ? my * L * 4 : L) + 255) / 256 * 256 + offsets_bytes(L, os);
   if (sums_off) *sums_off = done_bytes;
   return done_bytes + std::max<int64_t>(1, scan_tiles_of(my * L)) * os;
 }
@@ -938,6 +943,10 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_of
   p.done = static_cast<uint32_t*>(ws);
   p.slow = static_cast<uint8_t*>(ws);  // my_size <= 64 only, where the cursors are not used
   OT* sums = reinterpret_cast<OT*>(static_cast<uint8_t*>(ws) + sums_off);
+  // offsets given, or formed here from the lengths (BA:167): the complete cumsum sits
+  // just below the tile sums, and the kernels read its inclusive part
+  OT* formed = reinterpret_cast<OT*>(reinterpret_cast<uint8_t*>(sums) - offsets_bytes(a->lengths_size, a->offset_size));
+  if (!a->offsets) p.offsets = formed + 1;
   p.L = a->lengths_size;
   p.N = a->num_indices;
   p.my_size = a->my_size;
@@ -959,6 +968,20 @@ int run(const TbeBlockBucketizeArgs* a, hipStream_t s, void* ws, int64_t sums_of
   const int64_t row_blocks = std::max(std::min<int64_t>(std::max<int64_t>(1, (p.L + 3) / 4), 16LL * cus),
                                       (p.L + 15) / 16);
   const int64_t tiles = std::max<int64_t>(1, scan_tiles_of(nseg));
+  if (!a->offsets) {
+    // the scans below run after the count, so the two scans share the tile sums
+    const OT* len = static_cast<const OT*>(a->lengths);
+    const int64_t ltiles = std::max<int64_t>(1, scan_tiles_of(p.L));
+    hipLaunchKernelGGL(scan_tile_sums<OT>, dim3(static_cast<uint32_t>(ltiles)), dim3(kBBBlock), 0, s, len, p.L, sums);
+    if (ltiles <= kScanBaseMaxTiles) {
+      hipLaunchKernelGGL(scan_tiles_based<OT>, dim3(static_cast<uint32_t>(ltiles)), dim3(kBBBlock), 0, s, len, p.L,
+                         const_cast<const OT*>(sums), formed);
+    } else {
+      hipLaunchKernelGGL(scan_sums_exclusive<OT>, dim3(1), dim3(kBBBlock), 0, s, sums, ltiles);
+      hipLaunchKernelGGL(scan_tiles<OT>, dim3(static_cast<uint32_t>(ltiles)), dim3(kBBBlock), 0, s, len, p.L,
+                         const_cast<const OT*>(sums), formed);
+    }
+  }
   // counters and cursors in registers when every bucket fits a lane
   const bool reg = a->my_size <= kWaveBB;
   if (!reg)
@@ -1033,7 +1056,8 @@ int check_args(const TbeBlockBucketizeArgs* a) {
 }
 
 int check_pointers(const TbeBlockBucketizeArgs* a) {
-  if (!a->new_lengths || !a->new_offsets || (a->lengths_size > 0 && (!a->offsets || !a->block_sizes)) ||
+  if (!a->new_lengths || !a->new_offsets ||
+      (a->lengths_size > 0 && ((!a->offsets && !a->lengths) || !a->block_sizes)) ||
       (a->num_indices > 0 && (!a->indices || !a->new_indices)))
     return fail(TBE_ERR_INVALID_ARG, "null pointer argument");
   return TBE_OK;

@@ -369,7 +369,6 @@ block_bucketize_sparse_features_hip(const Tensor& lengths, const Tensor& indices
   Tensor new_lengths = at::empty({my_size * L}, lopt);
   Tensor new_offsets = at::empty({my_size * L + 1}, lopt);
   Tensor new_indices = at::empty({N}, iopt);
-  Tensor offsets = at::cumsum(len_c, 0, len_c.scalar_type()).contiguous();  // BA:167
   Tensor bso;
   if (batch_size_per_feature.has_value())  // BA:172: complete cumsum
     bso = at::cat({at::zeros({1}, lopt), at::cumsum(batch_size_per_feature->contiguous(), 0, len_c.scalar_type())}).contiguous();
@@ -405,7 +404,8 @@ block_bucketize_sparse_features_hip(const Tensor& lengths, const Tensor& indices
   TbeBlockBucketizeArgs a{};
   a.indices = idx_c.data_ptr();
   a.num_indices = N;
-  a.offsets = offsets.data_ptr();
+  a.offsets = nullptr;  // formed from the lengths by the library (BA:167)
+  a.lengths = len_c.data_ptr();
   a.lengths_size = L;
   a.index_size = static_cast<int32_t>(idx_c.element_size());
   a.offset_size = static_cast<int32_t>(len_c.element_size());

@@ -40,7 +40,7 @@ extern "C" {
  * every input index).
  *
  * Widths: index_size (indices, block_sizes, total_num_blocks, pos lists, new_indices,
- * new_pos, unbucketize_permute) and offset_size (offsets, batch_size_offsets,
+ * new_pos, unbucketize_permute) and offset_size (lengths, offsets, batch_size_offsets,
  * new_lengths, new_offsets), each 4 or 8.  Rows of a feature with a negative block
  * size, and indices whose bucket would fall outside [0, my_size) (only possible
  * with a total_num_blocks that is not a multiple of my_size), are left out; the
@@ -53,7 +53,8 @@ extern "C" {
 typedef struct TbeBlockBucketizeArgs {
   const void* indices;                 /* device [num_indices]                        */
   int64_t num_indices;
-  const void* offsets;                 /* device [lengths_size], inclusive cumsum     */
+  const void* offsets;                 /* device [lengths_size], inclusive cumsum,
+                                          or NULL with `lengths` given (see below)    */
   int64_t lengths_size;
   int32_t index_size;                  /* 4 or 8                                      */
   int32_t offset_size;                 /* 4 or 8                                      */
@@ -74,6 +75,10 @@ typedef struct TbeBlockBucketizeArgs {
   void* unbucketize_permute;           /* device [num_indices] or NULL                */
   void* workspace;
   int64_t workspace_bytes;
+  /* device [lengths_size] or NULL.  With offsets NULL the library forms the offsets
+   * from these lengths itself (the complete cumsum of BA:167) in its scratch, on the
+   * call's stream; with offsets given it is not read. */
+  const void* lengths;
 } TbeBlockBucketizeArgs;
 
 int64_t tbe_block_bucketize_workspace_bytes(int64_t my_size, int64_t lengths_size, int32_t offset_size);
@@ -94,6 +99,7 @@ int tbe_block_bucketize_sparse_features(const TbeBlockBucketizeArgs* args, void*
  * on holds until the process ends; it is cleared or fully written by the call's own
  * kernels where it must start at a known value.  A call needs
  *   roundup(my_size > 64 ? 4 * my_size * lengths_size : lengths_size, 256)
+ *   + roundup(offset_size * (lengths_size + 1), 256)
  *   + offset_size * max(1, ceil(my_size * lengths_size / 1024))
  * bytes of it; larger calls are rejected with TBE_ERR_UNSUPPORTED and a message.
  * Every call on one GPU shares that GPU's array, so calls on one GPU are made

@@ -1,7 +1,7 @@
 """GPU: tbe_block_bucketize_sparse_features_noalloc (no allocation, static scratch)
 gives exactly the outputs of tbe_block_bucketize_sparse_features (workspace
 argument), through the C ABI, on two calls in a row, the second with a smaller
-input, for register-cursor (my_size <= 64) and memory-cursor (my_size > 64)
+input (the first given lengths, the second offsets), for register-cursor (my_size <= 64) and memory-cursor (my_size > 64)
 bucket counts; a call that needs more scratch than the library holds is rejected."""
 import numpy as np
 import pytest
@@ -16,14 +16,14 @@ WIDE = Case("i64_rank100", 6, 512, 0, 96, 4, 8, 100, np.int64)
 WIDE_SMALL = Case("i32_rank70", 3, 64, 0, 40, 2, 6, 70, np.int32)
 
 
-def _run(gpu, case, seed, noalloc, weights, bucketize_pos, sequence, pos):
+def _run(gpu, case, seed, noalloc, weights, bucketize_pos, sequence, pos, pass_offsets=True):
     from fbgemm_ascend_amd import capi
     lengths, indices, block_sizes, w = gen_case(case, seed, weights)
     d = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
     plist = [d(p) for p in gen_bucketize_pos(block_sizes, case.my_size, seed)] if pos else None
     outs, new_off = capi.block_bucketize_sparse_features(
         d(lengths), d(indices), bucketize_pos, sequence, d(block_sizes), case.my_size, weights=d(w),
-        block_bucketize_pos=plist, noalloc=noalloc)
+        block_bucketize_pos=plist, noalloc=noalloc, pass_offsets=pass_offsets)
     torch.cuda.synchronize()
     return [None if o is None else o.cpu() for o in outs] + [new_off.cpu()]
 
@@ -44,7 +44,9 @@ def test_noalloc_matches_workspace_entry(pkg, gpu, big, small, weights, bucketiz
         seed = 100 + step
         print(f"[gpu] noalloc call {step + 1}: {name} my_size={case.my_size} w={weights} pos={bucketize_pos} "
               f"seq={sequence} poslist={pos}", flush=True)
-        got = _run(gpu, case, seed, True, weights, bucketize_pos, sequence, pos)
+        # the first call hands over the lengths (the library forms the offsets in its
+        # scratch), the second their cumsum
+        got = _run(gpu, case, seed, True, weights, bucketize_pos, sequence, pos, pass_offsets=step == 1)
         want = _run(gpu, case, seed, False, weights, bucketize_pos, sequence, pos)
         for n, g, e in zip(names, got, want):
             assert (g is None) == (e is None), n
