@@ -267,12 +267,13 @@ def _fp8_params():
     return out
 
 
-@pytest.mark.parametrize("kernel", ["default", "stream"])
+# (nobag has one kernel per group: no forced row-stream run of pooling NONE)
+_FP8_CASES = [(k,) + c for k in ("default", "stream") for c in _fp8_params() if not (k == "stream" and c[2] == 2)]
+
+
 @pytest.mark.parametrize("T", [1, 3])
-@pytest.mark.parametrize("eb,bias,pm,weighted,idx_dtype,out_ty", _fp8_params())
+@pytest.mark.parametrize("kernel,eb,bias,pm,weighted,idx_dtype,out_ty", _FP8_CASES)
 def test_fp8_exponent_params(pkg, oracle, gpu, T, eb, bias, pm, weighted, idx_dtype, out_ty, kernel):
-    if kernel == "stream" and pm == 2:
-        pytest.skip("nobag has one kernel per group")
     seed = (eb * 131 + bias * 7 + pm * 3 + T) & 0xFFFF
     m, idx, off, psw = _fp8_case(pkg, gpu, seed, T, eb, bias, pm, weighted, idx_dtype, out_ty)
     flags = pkg.capi.TBE_FLAG_FORCE_STREAM if kernel == "stream" else None
